@@ -1,0 +1,4 @@
+// Single translation unit of the ds41 gfx950 library: every kernel shares the
+// file-scope device status word without relocatable device code.
+#include "moe_kernels.inc"
+#include "moe_layer.inc"

@@ -1,0 +1,196 @@
+// Device-side building blocks shared by the gfx950 MoE kernels: MX scalar
+// formats, bf16 rounding, and the 16-channel MXFP4 x MXFP8 GEMV tile on the
+// CDNA4 scaled MFMA (V_MFMA_SCALE_F32_16X16X128_F8F6F4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "ds41_moe_gfx950.h"
+
+namespace ds41g {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+static_assert(sizeof(ds41_device_expert) == 64, "DeviceExpert must stay 64 bytes");
+static_assert(sizeof(ds41_gemm_job) == 32, "GemmJob must stay 32 bytes");
+
+constexpr int kMaxJobTokens = 8;   // rows per expert job (reference GemmJob: 1..8)
+constexpr int kWave = 64;
+
+// Kernel-visible status bits (ds41_status): a bounded wait that gave up, or a
+// job descriptor whose row count is outside 1..kMaxJobTokens.
+enum : uint32_t { kStatusReadyTimeout = 1u, kStatusBadJob = 2u, kStatusBadRoute = 4u };
+extern __device__ uint32_t ds41_status;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+
+// Round-to-nearest-even to bf16; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// E8M0 -> fp32: 2^(e-127), e == 0 -> 2^-127, e == 255 -> NaN.
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+  return e == 0 ? __uint_as_float(0x00400000u) : e == 255 ? __uint_as_float(0x7fffffffu)
+                                                            : __uint_as_float(e << 23);
+}
+
+// fp32 -> OCP E4M3 (fn), round-to-nearest-even, saturating at +-448, NaN -> 0x7f.
+// Integer formulation: the result never depends on the hardware converter's
+// rounding or NaN conventions.
+__device__ __forceinline__ uint32_t e4m3_from_f32(float v) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return 0x7fu;
+  if (a >= 0x43e00000u) return sign | 0x7eu;                 // |v| >= 448
+  if (a < 0x3c800000u) {                                     // |v| < 2^-6: grid of 2^-9
+    float m = __builtin_rintf(__uint_as_float(a) * 512.0f);  // exact scaling, ties-to-even
+    return sign | (uint32_t)m;
+  }
+  int e = (int)(a >> 23) - 127;
+  uint32_t mant = a & 0x7fffffu, r = mant >> 20, rem = mant & 0xfffffu;
+  r += (rem > 0x80000u || (rem == 0x80000u && (r & 1u))) ? 1u : 0u;
+  if (r == 8u) { r = 0u; ++e; }
+  if (e > 8 || (e == 8 && r > 6u)) return sign | 0x7eu;
+  return sign | (uint32_t)(((e + 7) << 3) | (int)r);
+}
+
+// MXFP8 scale exponent of a 32-group from its amax (mxfp4.cu:16-19):
+// e = ceil-to-power-of-two exponent of fp32(max(amax, 1e-4) * (1/448)).
+__device__ __forceinline__ uint32_t mxfp8_exponent(float amax) {
+  amax = fmaxf(amax, 1e-4f);
+  uint32_t b = __float_as_uint(amax * (1.0f / 448.0f));
+  return (b >> 23) + ((b & 0x7fffffu) != 0u);
+}
+
+// Bounded acquire-wait on a residency flag (mxfp4.cu:36-43 semantics). Returns
+// false after ~2 s without the expected generation, so no wave can spin forever.
+__device__ __forceinline__ bool wait_ready(const ds41_device_expert &e) {
+  if (!e.ready) return true;
+  for (uint32_t i = 0; i < (1u << 25); ++i) {
+    uint32_t v = __hip_atomic_load(e.ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    if (v == e.generation) return true;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  atomicOr(&ds41_status, kStatusReadyTimeout);
+  return false;
+}
+
+__device__ __forceinline__ const uint8_t *proj_weight(const ds41_device_expert &e, int p) {
+  return p == 0 ? e.gate : p == 1 ? e.up : e.down;
+}
+__device__ __forceinline__ const uint8_t *proj_scale(const ds41_device_expert &e, int p) {
+  return p == 0 ? e.gate_scale : p == 1 ? e.up_scale : e.down_scale;
+}
+
+// LDS image of the activation rows of one job: rows of `stride` bytes holding
+// E4M3 values zero-padded to a multiple of 128, and rows of `sstride` E8M0
+// scale bytes padded with 127.
+struct XTile {
+  const uint8_t *q, *s;
+  int stride, sstride, tokens;
+};
+
+__device__ __forceinline__ int chunks_of(int k) { return (k + 127) >> 7; }
+__device__ __host__ __forceinline__ int xtile_stride(int k) { return ((k + 127) / 128) * 128 + 16; }
+__device__ __host__ __forceinline__ int xtile_sstride(int k) { return ((k + 127) / 128) * 4; }
+
+// Stage `tokens` activation rows into LDS: LDS row r is source row row_idx(r) of
+// the E4M3 matrix x [*][k] and its scales xs [*][k/32]. Caller syncs.
+template <class RowIdx>
+__device__ __forceinline__ void stage_xtile(uint8_t *lq, uint8_t *ls, const uint8_t *x,
+                                            const uint8_t *xs, int k, int tokens, RowIdx row_idx) {
+  const int stride = xtile_stride(k), sstride = xtile_sstride(k);
+  const int pieces = (stride - 16) >> 4;
+  const bool aligned = ((((uintptr_t)x) | (uintptr_t)k) & 15u) == 0;
+  for (int p = threadIdx.x; p < tokens * pieces; p += blockDim.x) {
+    int r = p / pieces, off = (p - r * pieces) << 4;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    const uint8_t *src = x + (size_t)row_idx(r) * k + off;
+    if (off < k) {
+      if (aligned) v = *reinterpret_cast<const uint4 *>(src);
+      else {
+        uint8_t b[16];
+        for (int i = 0; i < 16; ++i) b[i] = src[i];
+        v = *reinterpret_cast<const uint4 *>(b);
+      }
+    }
+    *reinterpret_cast<uint4 *>(lq + r * stride + off) = v;
+  }
+  const int ng = k >> 5;
+  for (int p = threadIdx.x; p < tokens * sstride; p += blockDim.x) {
+    int r = p / sstride, g = p - r * sstride;
+    ls[r * sstride + g] = g < ng ? xs[(size_t)row_idx(r) * ng + g] : (uint8_t)127;
+  }
+}
+
+// One wave computes out[t][row0 + j] for j < 16, t < tokens over the full K.
+// Operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950):
+//   B (fp4 weights, 128 x 16): lane l holds 32 consecutive k = 32*(l>>4) .. +31 of
+//     column l&15, low nibble first -> one 16-byte load of the weight row;
+//   A (fp8 activations, 16 x 128): lane l holds row l&15, bytes 0..15 = k 16q..16q+15
+//     and bytes 16..31 = k 64+16q..64+16q+15 with q = l>>4;
+//   scales: lane l carries the E8M0 of row/column l&15 for k-block l>>4 (byte 0);
+//   D (16 x 16 fp32): lane l holds column l&15, rows 4*(l>>4) + r in register r.
+// A = activations (tokens as rows), B = weights (channels as columns), so lane l
+// ends with channel l&15 for tokens 4*(l>>4) .. +3.
+template <int U, bool Aligned16>
+__device__ __forceinline__ v4f gemv16(const uint8_t *__restrict__ wrow, const uint8_t *__restrict__ srow,
+                                      bool row_ok, int k, const XTile &x) {
+  const int lane = threadIdx.x & 63, kb = lane >> 4, i = lane & 15;
+  const int ng = k >> 5, nch = chunks_of(k);
+  const bool a_ok = i < x.tokens;
+  const uint8_t *xa = x.q + i * x.stride + 16 * kb;
+  const uint8_t *sa = x.s + i * x.sstride + kb;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  uint4 b[U], nb[U];
+  uint32_t bs[U], nbs[U];
+  auto load = [&](int c0, uint4 *dst, uint32_t *dsts) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int g = 4 * (c0 + u) + kb;
+      const bool ok = row_ok && g < ng;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (ok) {
+        if (Aligned16) v = *reinterpret_cast<const uint4 *>(wrow + 16 * g);
+        else {
+          uint2 lo = *reinterpret_cast<const uint2 *>(wrow + 16 * g);
+          uint2 hi = *reinterpret_cast<const uint2 *>(wrow + 16 * g + 8);
+          v = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+      }
+      dst[u] = v;
+      dsts[u] = ok ? (uint32_t)srow[g] : 127u;
+    }
+  };
+  load(0, b, bs);
+  for (int c0 = 0; c0 < nch; c0 += U) {
+    if (c0 + U < nch) load(c0 + U, nb, nbs);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u;
+      if (c < nch) {
+        v8i a = {0, 0, 0, 0, 0, 0, 0, 0};
+        int as = 127;
+        if (a_ok) {
+          uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * c);
+          uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * c + 64);
+          a = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+          as = sa[4 * c];
+        }
+        v8i bv = v8i{(int)b[u].x, (int)b[u].y, (int)b[u].z, (int)b[u].w, 0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bv, acc, 0, 4, 0, as, 0, (int)bs[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) { b[u] = nb[u]; bs[u] = nbs[u]; }
+  }
+  return acc;
+}
+
+}  // namespace ds41g

@@ -1,0 +1,236 @@
+"""ctypes binding of libds41_gfx950.so (the gfx950 verify-path library).
+
+The C ABI (include/ds41_moe_gfx950.h, include/ds41_accept_gfx950.h) takes plain
+device pointers; torch is used here only to own device memory and streams.
+Every call raises if the library is missing or returns a HIP error: there is
+no CPU fallback.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libds41_gfx950.so")
+_lib = None
+
+PROJ_GATE, PROJ_UP, PROJ_DOWN = 0, 1, 2
+
+
+class DeviceExpert(ctypes.Structure):
+    """components/moe/include/ds41/store.hpp:110-117 (64 bytes)."""
+    _fields_ = [("gate", ctypes.c_void_p), ("gate_scale", ctypes.c_void_p),
+                ("up", ctypes.c_void_p), ("up_scale", ctypes.c_void_p),
+                ("down", ctypes.c_void_p), ("down_scale", ctypes.c_void_p),
+                ("ready", ctypes.c_void_p), ("generation", ctypes.c_uint32),
+                ("slot", ctypes.c_int32)]
+
+
+class GemmJob(ctypes.Structure):
+    """components/moe/include/ds41/kernels.cuh:8-13 (32 bytes)."""
+    _fields_ = [("expert", ctypes.c_uint32), ("tokens", ctypes.c_int32),
+                ("x", ctypes.c_void_p), ("x_scale", ctypes.c_void_p),
+                ("output", ctypes.c_void_p)]
+
+
+class MoeLayerArgs(ctypes.Structure):
+    _fields_ = [("x_bf16", ctypes.c_void_p), ("router_w", ctypes.c_void_p),
+                ("router_bias", ctypes.c_void_p), ("table", ctypes.c_void_p),
+                ("expert_base", ctypes.c_int32), ("shared_index", ctypes.c_int32),
+                ("tokens", ctypes.c_int32), ("hidden", ctypes.c_int32),
+                ("inter", ctypes.c_int32), ("n_experts", ctypes.c_int32),
+                ("topk", ctypes.c_int32), ("score_mode", ctypes.c_int32),
+                ("route_scale", ctypes.c_float), ("swiglu_limit", ctypes.c_float),
+                ("y_bf16", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_size_t), ("ids_out", ctypes.c_void_p),
+                ("weights_out", ctypes.c_void_p), ("logits_out", ctypes.c_void_p)]
+
+
+assert ctypes.sizeof(DeviceExpert) == 64 and ctypes.sizeof(GemmJob) == 32
+
+
+class SparkResult(ctypes.Structure):
+    """engine/third_party/spark/include/ds41/spark.h ds41_spark_result."""
+    _fields_ = [("tokens", ctypes.c_int32 * 6), ("emitted", ctypes.c_int),
+                ("accepted_drafts", ctypes.c_int), ("accepted_input_rows", ctypes.c_int),
+                ("rejected", ctypes.c_int)]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
+        _lib = ctypes.CDLL(LIB_PATH)
+        _lib.ds41_moe_layer_workspace_bytes.restype = ctypes.c_size_t
+        _lib.ds41_gfx950_version.restype = ctypes.c_char_p
+    return _lib
+
+
+def check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with hipError {rc}")
+
+
+def _p(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def take_status():
+    v = ctypes.c_uint32(0)
+    check(lib().ds41_take_status(ctypes.byref(v)), "ds41_take_status")
+    return v.value
+
+
+# ---- formats -------------------------------------------------------------------
+def quantize_mxfp8(x, stream=None):
+    import torch
+    rows, cols = x.shape
+    q = torch.empty((rows, cols), dtype=torch.uint8, device=x.device)
+    s = torch.empty((rows, cols // 32), dtype=torch.uint8, device=x.device)
+    check(lib().ds41_quantize_mxfp8(_p(x), _p(q), _p(s), rows, cols, _stream(stream)), "quantize_mxfp8")
+    return q, s
+
+
+def dequant_mxfp4(w, s, n, k, stream=None):
+    import torch
+    out = torch.empty((n, k), dtype=torch.float32, device=w.device)
+    check(lib().ds41_dequant_mxfp4(_p(w), _p(s), _p(out), n, k, _stream(stream)), "dequant_mxfp4")
+    return out
+
+
+# ---- projections ----------------------------------------------------------------
+def mxfp4_raw(w, ws, xq, xs, m, n, k, out=None, stream=None):
+    """ds41_mxfp4_native_parallel_raw: out[m][n] bf16."""
+    import torch
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=w.device)
+    check(lib().ds41_mxfp4_native_parallel_raw(_p(w), _p(ws), _p(xq), _p(xs), _p(out), m, n, k,
+                                               _stream(stream)), "mxfp4_raw")
+    return out
+
+
+def device_table(experts, device="cuda"):
+    """experts: list of dicts with gate, gate_scale, up, up_scale, down, down_scale tensors
+    (or None entries). Returns (device uint8 tensor holding DeviceExpert[len], host array)."""
+    import torch
+    arr = (DeviceExpert * len(experts))()
+    for i, e in enumerate(experts):
+        if e is None:
+            continue
+        for f in ("gate", "gate_scale", "up", "up_scale", "down", "down_scale"):
+            t = e.get(f)
+            setattr(arr[i], f, 0 if t is None else t.data_ptr())
+        arr[i].ready = e.get("ready", 0) or 0
+        arr[i].generation = e.get("generation", 0)
+        arr[i].slot = e.get("slot", i)
+    raw = bytes(arr)
+    host = torch.frombuffer(bytearray(raw), dtype=torch.uint8)
+    return host.to(device), arr
+
+
+def device_jobs(jobs, device="cuda"):
+    import torch
+    arr = (GemmJob * len(jobs))()
+    for i, (expert, tokens, x, xs, out) in enumerate(jobs):
+        arr[i].expert, arr[i].tokens = expert, tokens
+        arr[i].x, arr[i].x_scale, arr[i].output = x.data_ptr(), xs.data_ptr(), out.data_ptr()
+    host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+    return host.to(device)
+
+
+def grouped(table, jobs, count, projection, n, k, entry="ds41_grouped_mxfp4_native_parallel", stream=None):
+    check(getattr(lib(), entry)(_p(table), _p(jobs), count, projection, n, k, _stream(stream)), entry)
+
+
+def swiglu(g, u, w, limit, stream=None):
+    import torch
+    rows, cols = g.shape
+    out = torch.empty_like(g)
+    check(lib().ds41_swiglu(_p(g), _p(u), _p(w), _p(out), rows, cols, ctypes.c_float(limit), _stream(stream)),
+          "swiglu")
+    return out
+
+
+def reduce_experts(routed, ids, shared, stream=None):
+    import torch
+    rows, topk, hidden = routed.shape
+    out = torch.empty((rows, hidden), dtype=torch.bfloat16, device=routed.device)
+    check(lib().ds41_reduce_experts(_p(routed), _p(ids), _p(shared), _p(out), rows, topk, hidden,
+                                    _stream(stream)), "reduce_experts")
+    return out
+
+
+# ---- router ---------------------------------------------------------------------
+def router_logits(x, w, stream=None):
+    import torch
+    M, K = x.shape
+    N = w.shape[0]
+    out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    check(lib().ds41_router_logits(_p(x), _p(w), _p(out), M, N, K, _stream(stream)), "router_logits")
+    return out
+
+
+def router_scores(logits, bias, stream=None):
+    import torch
+    M, N = logits.shape
+    u = torch.empty_like(logits)
+    b = torch.empty_like(logits)
+    check(lib().ds41_dense_router_scores(_p(logits), _p(bias), _p(u), _p(b), M, N, _stream(stream)),
+          "router_scores")
+    return u, b
+
+
+def router_topk(b, k, stream=None):
+    import torch
+    M, N = b.shape
+    ids = torch.empty((M, k), dtype=torch.int32, device=b.device)
+    check(lib().ds41_router_topk(_p(b), _p(ids), M, N, k, _stream(stream)), "router_topk")
+    return ids
+
+
+def router_weights(u, ids, scale=1.5, stream=None):
+    import torch
+    M, N = u.shape
+    k = ids.shape[1]
+    w = torch.empty((M, k), dtype=torch.float32, device=u.device)
+    check(lib().ds41_dense_router_weights(_p(u), _p(ids), _p(w), M, N, k, ctypes.c_float(scale),
+                                          _stream(stream)), "router_weights")
+    return w
+
+
+# ---- fused layer ------------------------------------------------------------------
+def layer_workspace_bytes(T, H, I, E, K):
+    return lib().ds41_moe_layer_workspace_bytes(T, H, I, E, K)
+
+
+def make_layer_args(x, router_w, router_bias, table, expert_base, shared_index, T, H, I, E, K, y,
+                    workspace, score_mode=0, route_scale=1.5, swiglu_limit=10.0, ids_out=None,
+                    weights_out=None, logits_out=None):
+    a = MoeLayerArgs()
+    a.x_bf16, a.router_w, a.router_bias, a.table = x.data_ptr(), router_w.data_ptr(), \
+        router_bias.data_ptr(), table.data_ptr()
+    a.expert_base, a.shared_index = expert_base, shared_index
+    a.tokens, a.hidden, a.inter, a.n_experts, a.topk = T, H, I, E, K
+    a.score_mode, a.route_scale, a.swiglu_limit = score_mode, route_scale, swiglu_limit
+    a.y_bf16, a.workspace, a.workspace_bytes = y.data_ptr(), workspace.data_ptr(), workspace.numel()
+    a.ids_out = 0 if ids_out is None else ids_out.data_ptr()
+    a.weights_out = 0 if weights_out is None else weights_out.data_ptr()
+    a.logits_out = 0 if logits_out is None else logits_out.data_ptr()
+    return a
+
+
+def moe_layer(args, stream=None):
+    check(lib().ds41_moe_verify_layer(ctypes.byref(args), _stream(stream)), "moe_verify_layer")
+
+
+def layer_plan(workspace, T, H, I, E, K):
+    ids = (ctypes.c_int32 * (T * K + 1))()
+    n = lib().ds41_moe_layer_plan(ctypes.c_void_p(workspace.data_ptr()), T, H, I, E, K, ids, T * K + 1)
+    if n < 0:
+        raise RuntimeError("ds41_moe_layer_plan failed")
+    return list(ids[:n])

@@ -1,0 +1,163 @@
+/*
+ * ds41 speculative-verify MoE path for MI355X (gfx950): C ABI.
+ *
+ * Drop-in replacements for the reference's components/moe kernel API and its
+ * raw C entry points, implemented with hand-written HIP kernels (scaled
+ * f8f6f4 MFMA GEMV/GEMM) for gfx950. All buffers are caller-owned DEVICE
+ * memory unless stated; `stream` is a hipStream_t passed as void*. Every entry
+ * returns a hipError_t value as int (0 == hipSuccess); invalid arguments
+ * return hipErrorInvalidValue (1), as the reference returns
+ * cudaErrorInvalidValue. No entry point allocates or synchronises unless its
+ * comment says so.
+ *
+ * Reference citations are paths in SSHdotCodes/deepseek-v4.1-flash-pro6000.
+ */
+#ifndef DS41_MOE_GFX950_H
+#define DS41_MOE_GFX950_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Device ABI types, byte-identical to the reference
+ * (components/moe/include/ds41/store.hpp:110-117 DeviceExpert, 64 B;
+ *  components/moe/include/ds41/kernels.cuh:8-13 GemmJob, 32 B).
+ * ready == NULL: ordering is the caller's (stream/event); otherwise kernels
+ * wait until *ready == generation (acquire) before reading the weights. */
+typedef struct ds41_device_expert {
+  const uint8_t *gate, *gate_scale;
+  const uint8_t *up, *up_scale;
+  const uint8_t *down, *down_scale;
+  const uint32_t *ready;
+  uint32_t generation;
+  int32_t slot;
+} ds41_device_expert;
+
+typedef struct ds41_gemm_job {
+  uint32_t expert;          /* index into the DeviceExpert table */
+  int32_t tokens;           /* 1..16 rows for this expert */
+  const uint8_t *x;         /* E4M3 [tokens][k] */
+  const uint8_t *x_scale;   /* E8M0 [tokens][k/32] */
+  void *output;             /* BF16 [tokens][n] */
+} ds41_gemm_job;
+
+enum { DS41_PROJ_GATE = 0, DS41_PROJ_UP = 1, DS41_PROJ_DOWN = 2 };
+
+/* ---- components/moe kernel API (kernels.cuh:14-38) -------------------------- */
+/* quantize_mxfp8 (components/moe/src/mxfp4.cu:341-345): bf16 [rows][cols] ->
+ * E4M3 q [rows][cols] + E8M0 s [rows][cols/32]. cols % 32 == 0. */
+int ds41_quantize_mxfp8(const void *x_bf16, uint8_t *q, uint8_t *scales, int rows, int cols,
+                        void *stream);
+/* grouped_mxfp4 / _native / _parallel / _native_parallel / _native_tiled
+ * (mxfp4.cu:346-381): one launch over `count` jobs of a W4A8 projection,
+ * out[t][n] = bf16(sum_k x[t][k] * w[n][k]). All five names run the same
+ * gfx950 kernel (fp32 accumulation on the scaled MFMA). k % 32 == 0. */
+int ds41_grouped_mxfp4(const ds41_device_expert *table, const ds41_gemm_job *jobs, int count,
+                       int projection, int n, int k, void *stream);
+int ds41_grouped_mxfp4_native(const ds41_device_expert *table, const ds41_gemm_job *jobs,
+                              int count, int projection, int n, int k, void *stream);
+int ds41_grouped_mxfp4_parallel(const ds41_device_expert *table, const ds41_gemm_job *jobs,
+                                int count, int projection, int n, int k, void *stream);
+int ds41_grouped_mxfp4_native_parallel(const ds41_device_expert *table,
+                                       const ds41_gemm_job *jobs, int count, int projection,
+                                       int n, int k, void *stream);
+int ds41_grouped_mxfp4_native_tiled(const ds41_device_expert *table, const ds41_gemm_job *jobs,
+                                    int count, int projection, int n, int k, void *stream);
+/* swiglu (mxfp4.cu:352-356): g=min(g,L), u=clamp(u,+-L) (L>0), h=silu(g)*u*w[row] -> bf16.
+ * route_weight may be NULL. */
+int ds41_swiglu(const void *gate_bf16, const void *up_bf16, const float *route_weight,
+                void *out_bf16, int rows, int cols, float limit, void *stream);
+/* reduce_experts (mxfp4.cu:386-389): per token, routed rows [rows][topk][hidden]
+ * summed in ascending expert-id order (fp32), + shared [rows][hidden] (nullable),
+ * -> bf16. Duplicate/invalid ids: the token's output row is set to NaN and the
+ * call still returns 0 (the reference traps the device instead). topk <= 8. */
+int ds41_reduce_experts(const void *routed_bf16, const int32_t *ids, const void *shared_bf16,
+                        void *out_bf16, int rows, int topk, int hidden, void *stream);
+
+/* ---- raw C ABI (kernels.cuh:43-62; mxfp4.cu:392-442) ------------------------ */
+int ds41_mxfp4_raw(const uint8_t *weight, const uint8_t *weight_scale, const uint8_t *activation,
+                   const uint8_t *activation_scale, void *output_bf16, int m, int n, int k,
+                   void *stream);
+int ds41_mxfp4_native_raw(const uint8_t *weight, const uint8_t *weight_scale,
+                          const uint8_t *activation, const uint8_t *activation_scale,
+                          void *output_bf16, int m, int n, int k, void *stream);
+int ds41_mxfp4_parallel_raw(const uint8_t *weight, const uint8_t *weight_scale,
+                            const uint8_t *activation, const uint8_t *activation_scale,
+                            void *output_bf16, int m, int n, int k, void *stream);
+int ds41_mxfp4_native_parallel_raw(const uint8_t *weight, const uint8_t *weight_scale,
+                                   const uint8_t *activation, const uint8_t *activation_scale,
+                                   void *output_bf16, int m, int n, int k, void *stream);
+int ds41_quantize_mxfp8_raw(const void *input_bf16, uint8_t *q, uint8_t *scales, int rows,
+                            int cols, void *stream);
+int ds41_swiglu_raw(const void *gate_bf16, const void *up_bf16, const float *route_weight,
+                    void *output_bf16, int rows, int cols, float limit, void *stream);
+
+/* ---- pluggable projection backend "xk" v1 (components/moe/include/ds41/decode_backend.hpp:7-22) */
+int ds41_xk_projection_abi_version(void); /* returns 1 */
+int ds41_xk_grouped_v1(const ds41_device_expert *table, const ds41_gemm_job *jobs, int count,
+                       int projection, int n, int k, void *stream);
+
+/* ---- router (components/dense/src/ops.cu:73,107,117; engine/src/ops.cu:59-73,126-130) */
+/* u = sqrt(z > 20 ? z : log1p(exp(z))), b = u + bias[col] over logits [M][N]. */
+int ds41_dense_router_scores(const float *logits, const float *bias, float *u, float *b, int M,
+                             int N, void *stream);
+/* w[row][i] = u[row][ids[i]] / (fixed-order sum + 1e-20) * scale, topk in {1..8}. */
+int ds41_dense_router_weights(const float *scores, const int32_t *ids, float *w, int M, int N,
+                              int topk, float scale, void *stream);
+/* engine/src/ops.cu:126-130: one row, scale 1.5. */
+int ds41_engine_route_weights(const float *scores, const int *ids, float *out, int k,
+                              void *stream);
+/* fp32 router GEMV (the reference's cuBLAS fp32 GEMV, batch.inc:23-41,460):
+ * logits[t][e] = sum_h bf16 x[t][h] * w[e][h]; M <= 16. */
+int ds41_router_logits(const void *x_bf16, const float *w, float *logits, int M, int N, int K,
+                       void *stream);
+/* Top-k by biased score, descending, ties -> lower id (batch.inc:228-237). M rows of N <= 1024. */
+int ds41_router_topk(const float *b, int32_t *ids, int M, int N, int topk, void *stream);
+
+/* ---- fused verify MoE layer (batch.inc:220-335 bmoe + bshared) ------------- */
+/* One MoE layer for T = tokens rows, entirely on the device with no host sync:
+ * router GEMV + score, top-k + route weights + route plan, MXFP8 quant,
+ * fused gate/up MXFP4 GEMV + SwiGLU(limit)*w + MXFP8, down GEMV, ordered reduce
+ * (ascending expert id, shared expert last). Routed experts are
+ * table[expert_base + id]; the shared expert is table[shared_index]
+ * (shared_index < 0: none). */
+typedef struct ds41_moe_layer_args {
+  const void *x_bf16;             /* [tokens][hidden] */
+  const float *router_w;          /* [n_experts][hidden] fp32 */
+  const float *router_bias;       /* [n_experts] fp32 */
+  const ds41_device_expert *table;
+  int32_t expert_base, shared_index;
+  int32_t tokens, hidden, inter, n_experts, topk;
+  int32_t score_mode;             /* 0: sqrt-softplus (reference), 1: sigmoid */
+  float route_scale;              /* 1.5 in the reference */
+  float swiglu_limit;             /* 10 in the reference */
+  void *y_bf16;                   /* [tokens][hidden] */
+  void *workspace;                /* ds41_moe_layer_workspace_bytes() device bytes */
+  size_t workspace_bytes;
+  int32_t *ids_out;               /* optional [tokens][topk] (device) */
+  float *weights_out;             /* optional [tokens][topk] (device) */
+  float *logits_out;              /* optional [tokens][n_experts] (device) */
+} ds41_moe_layer_args;
+size_t ds41_moe_layer_workspace_bytes(int tokens, int hidden, int inter, int n_experts,
+                                      int topk);
+int ds41_moe_verify_layer(const ds41_moe_layer_args *args, void *stream);
+/* Reads the route plan of the last layer call from its workspace (host copy, synchronous):
+ * unique expert count and ids; returns the count or -1. */
+int ds41_moe_layer_plan(const void *workspace, int tokens, int hidden, int inter, int n_experts,
+                        int topk, int32_t *unique_ids, int max_ids);
+
+/* MXFP4 dequantisation: w [n][k/2] + s [n][k/32] -> fp32 [n][k] (bit-exact). */
+int ds41_dequant_mxfp4(const uint8_t *w, const uint8_t *s, float *out, int n, int k,
+                       void *stream);
+
+/* Library version string. */
+const char *ds41_gfx950_version(void);
+/* Reads and clears the kernels' status bits (synchronous): 1 a residency wait
+ * gave up, 2 a job's row count was outside 1..8, 4 invalid/duplicate routes. */
+int ds41_take_status(uint32_t *status);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
