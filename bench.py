@@ -1,0 +1,181 @@
+"""Benchmark of the ds41 speculative-verify MoE path on one MI355X.
+
+Default workload: one MoE layer decode verify with
+T=4 rows (1 committed + 3 MTP drafts), hidden 4096, 384 routed experts
+(intermediate 2880, MXFP4 e2m1 + e8m0/32) top-6 + 1 shared expert, all
+resident in HBM; router fp32 N(0, 0.02^2), inputs bf16 N(0, 1). A step is one
+layer pass over one batch of T rows. Inputs rotate over a pool of 64 seeded
+activations so routing (and the experts read) changes from step to step.
+
+Prints ONE JSON line (the driver's contract) with a roofline object for the
+dominant kernel (fused gate/up/activation GEMV), timed live with HIP events on
+the launch stream, and a cpu_baseline object: the C oracle running the same
+layer on the host cores (rank 0, N=1, a bounded sample).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "deepseek-v4.1-flash-pro6000_amd"), os.path.join(ROOT, "oracle")):
+    sys.path.insert(0, _p)
+
+EXPERT_BYTES = 18_800_640          # gate + up + down weights and E8M0 scales (H=4096, I=2880)
+GATE_UP_BYTES = 2 * (2880 * 2048 + 2880 * 128)
+DOWN_BYTES = 4096 * 1440 + 4096 * 90
+PEAK_HBM_GBPS = 8000.0
+METRIC = "verify tokens/s per MTP step (T=1+k); MoE HBM GB/s as % of 8 TB/s peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(x_np, wg_np, bias_np, experts_gpu, H, I, E, seconds):
+    """The C oracle (a port of the reference arithmetic) on all host cores: one full
+    layer (router, top-6, MXFP8, 25 expert FFNs, reduce) per sample."""
+    import numpy as np
+    import oracle as O
+    threads = len(os.sched_getaffinity(0))
+    logits = O.router_logits(x_np, wg_np)
+    u, b = O.router_scores(logits, bias_np)
+    ids = O.topk(b, 6)
+    experts_np = [None] * E
+    for e in sorted(set(ids.ravel().tolist())):
+        experts_np[e] = {k: v.cpu().numpy() for k, v in experts_gpu[e].items()}
+    shared_np = {k: v.cpu().numpy() for k, v in experts_gpu[E].items()}
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        O.moe_layer(x_np, wg_np, bias_np, experts_np, shared_np, H, I, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end:
+            break
+    T = x_np.shape[0]
+    per = sum(times) / len(times)
+    return {"value": T / per, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} full layer passes (T={T}, {len(set(ids.ravel().tolist()))} routed experts + "
+                      f"shared) of the C oracle, {per * 1e3:.1f} ms each"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the verify path "
+              "is a single-GPU workload here and multi-GPU sharding is design-only.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import ds41_gfx950 as G
+    import oracle as O
+
+    gpu = torch.device("cuda:0")
+    T, H, I, E, K = 4, 4096, 2880, 384, 6
+    log(f"bench: config1 one MoE layer T={T} H={H} I={I} E={E}+1 shared, steps={args.steps} warmup={args.warmup}")
+    g = torch.Generator(device=gpu).manual_seed(0)
+
+    def rnd(shape, lo, hi):
+        return torch.randint(lo, hi, shape, dtype=torch.uint8, device=gpu, generator=g)
+
+    # e2m1 nibbles uniform over 16 codes (bytes uniform), e8m0 scales uniform over 2^-8..2^-4
+    P = dict(gate=rnd((E + 1, I, H // 2), 0, 256), gate_scale=rnd((E + 1, I, H // 32), 119, 124),
+             up=rnd((E + 1, I, H // 2), 0, 256), up_scale=rnd((E + 1, I, H // 32), 119, 124),
+             down=rnd((E + 1, H, I // 2), 0, 256), down_scale=rnd((E + 1, H, I // 32), 119, 124))
+    experts = [{k: v[e] for k, v in P.items()} for e in range(E + 1)]
+    table, _ = G.device_table(experts, gpu)
+    rng = np.random.default_rng(0)
+    pool = 64
+    x_pool_np = [O.bf16_bits(rng.standard_normal((T, H)).astype(np.float32)) for _ in range(pool)]
+    x_pool = torch.stack([torch.from_numpy(a.view(np.int16)) for a in x_pool_np]).to(gpu).view(torch.bfloat16)
+    wg_np = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    bias_np = np.zeros(E, np.float32)
+    wg, bias = torch.from_numpy(wg_np).to(gpu), torch.from_numpy(bias_np).to(gpu)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
+    ws = torch.empty(G.layer_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
+    layer_args = [G.make_layer_args(x_pool[i], wg, bias, table, 0, E, T, H, I, E, K, y, ws) for i in range(pool)]
+    stream = torch.cuda.current_stream()
+
+    # unique routed experts per pool entry (bytes actually streamed per step)
+    uniq = []
+    for i in range(pool):
+        G.moe_layer(layer_args[i], stream)
+        uniq.append(len(G.layer_plan(ws, T, H, I, E, K)))
+    torch.cuda.synchronize()
+    assert G.take_status() == 0
+
+    for i in range(args.warmup):
+        G.moe_layer(layer_args[i % pool], stream)
+    torch.cuda.synchronize()
+
+    ev = G.Events(2)
+    torch.cuda.synchronize()
+    ev.record(0, stream)
+    for i in range(args.steps):
+        G.moe_layer(layer_args[i % pool], stream)
+    ev.record(1, stream)
+    torch.cuda.synchronize()
+    total_ms = ev.elapsed(0, 1)
+    ms_per_step = total_ms / args.steps
+
+    # per-kernel durations with stage events (a separate pass over the same steps)
+    stage = G.Events(6 * args.steps)
+    for i in range(args.steps):
+        a = layer_args[i % pool]
+        a.stage_events = stage.ptr(6 * i)
+        G.moe_layer(a, stream)
+        a.stage_events = None
+    torch.cuda.synchronize()
+    names = ["router_quant", "route_plan", "gate_up_act", "down", "reduce"]
+    stage_ms = {n: 0.0 for n in names}
+    gate_bytes = down_bytes = 0
+    for i in range(args.steps):
+        for j, n in enumerate(names):
+            stage_ms[n] += stage.elapsed(6 * i + j, 6 * i + j + 1)
+        u = uniq[i % pool]
+        gate_bytes += (u + 1) * GATE_UP_BYTES
+        down_bytes += (u + 1) * DOWN_BYTES
+    assert G.take_status() == 0
+    avg = {n: stage_ms[n] / args.steps for n in names}
+    gate_gbps = gate_bytes / (stage_ms["gate_up_act"] * 1e-3) / 1e9
+    down_gbps = down_bytes / (stage_ms["down"] * 1e-3) / 1e9
+    layer_bytes = sum((uniq[i % pool] + 1) * EXPERT_BYTES + E * H * 4 for i in range(args.steps))
+    layer_gbps = layer_bytes / (total_ms * 1e-3) / 1e9
+    log("stage avg us: " + ", ".join(f"{n} {avg[n] * 1e3:.1f}" for n in names))
+    log(f"gate_up_act {gate_gbps:.0f} GB/s, down {down_gbps:.0f} GB/s, layer {layer_gbps:.0f} GB/s "
+        f"({layer_gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s), mean unique experts {np.mean(uniq):.2f}")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(x_pool_np[0], wg_np, bias_np, experts, H, I, E, args.cpu_seconds)
+        log(f"cpu baseline: {cpu}")
+
+    out = {
+        "metric": METRIC, "value": T / (ms_per_step * 1e-3), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4 weights x mxfp8 activations, fp32 accumulate",
+        "data": "synthetic (seeded uniform e2m1/e8m0 weights, N(0,1) bf16 rows, random-init router)",
+        "config": {"workload": "configs[1]: one MoE layer decode verify, T=4 (1+3 MTP drafts), hidden 4096, "
+                               "384 routed experts (I=2880, MXFP4) top-6 + 1 shared, all HBM-resident",
+                   "tokens": T, "hidden": H, "inter": I, "experts": E, "topk": K,
+                   "mean_unique_experts": float(np.mean(uniq))},
+        "hbm_gbps": layer_gbps, "hbm_frac": layer_gbps / PEAK_HBM_GBPS,
+        "stage_us": {n: avg[n] * 1e3 for n in names},
+        "roofline": {"bound": "hbm", "kernel": "layer_gate_up_act_kernel", "achieved": gate_gbps,
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": gate_gbps / PEAK_HBM_GBPS, "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

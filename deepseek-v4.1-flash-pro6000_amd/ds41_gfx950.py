@@ -41,7 +41,8 @@ class MoeLayerArgs(ctypes.Structure):
                 ("route_scale", ctypes.c_float), ("swiglu_limit", ctypes.c_float),
                 ("y_bf16", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_size_t), ("ids_out", ctypes.c_void_p),
-                ("weights_out", ctypes.c_void_p), ("logits_out", ctypes.c_void_p)]
+                ("weights_out", ctypes.c_void_p), ("logits_out", ctypes.c_void_p),
+                ("stage_events", ctypes.c_void_p)]
 
 
 assert ctypes.sizeof(DeviceExpert) == 64 and ctypes.sizeof(GemmJob) == 32
@@ -226,6 +227,33 @@ def make_layer_args(x, router_w, router_bias, table, expert_base, shared_index, 
 
 def moe_layer(args, stream=None):
     check(lib().ds41_moe_verify_layer(ctypes.byref(args), _stream(stream)), "moe_verify_layer")
+
+
+class Events:
+    """n hipEvents owned by the library (timing on a given stream)."""
+
+    def __init__(self, n):
+        self.n = n
+        self.arr = (ctypes.c_void_p * n)()
+        check(lib().ds41_events_create(self.arr, n), "ds41_events_create")
+
+    def ptr(self, i=0):
+        return ctypes.cast(ctypes.byref(self.arr, i * ctypes.sizeof(ctypes.c_void_p)), ctypes.c_void_p).value
+
+    def record(self, i, stream=None):
+        check(lib().ds41_event_record(ctypes.c_void_p(self.arr[i]), _stream(stream)), "ds41_event_record")
+
+    def elapsed(self, i, j):
+        ms = ctypes.c_float(0)
+        check(lib().ds41_event_elapsed_ms(ctypes.c_void_p(self.arr[i]), ctypes.c_void_p(self.arr[j]),
+                                          ctypes.byref(ms)), "ds41_event_elapsed_ms")
+        return ms.value
+
+    def __del__(self):
+        try:
+            lib().ds41_events_destroy(self.arr, self.n)
+        except Exception:
+            pass
 
 
 def layer_plan(workspace, T, H, I, E, K):

@@ -138,6 +138,8 @@ typedef struct ds41_moe_layer_args {
   int32_t *ids_out;               /* optional [tokens][topk] (device) */
   float *weights_out;             /* optional [tokens][topk] (device) */
   float *logits_out;              /* optional [tokens][n_experts] (device) */
+  void *const *stage_events;      /* optional: 6 hipEvent_t recorded on `stream` before each of
+                                     the 5 kernels and after the last (for per-kernel timing) */
 } ds41_moe_layer_args;
 size_t ds41_moe_layer_workspace_bytes(int tokens, int hidden, int inter, int n_experts,
                                       int topk);
@@ -150,6 +152,12 @@ int ds41_moe_layer_plan(const void *workspace, int tokens, int hidden, int inter
 /* MXFP4 dequantisation: w [n][k/2] + s [n][k/32] -> fp32 [n][k] (bit-exact). */
 int ds41_dequant_mxfp4(const uint8_t *w, const uint8_t *s, float *out, int n, int k,
                        void *stream);
+
+/* hipEvent helpers for timing from hosts without HIP bindings. */
+int ds41_events_create(void **events, int n);
+int ds41_events_destroy(void **events, int n);
+int ds41_event_elapsed_ms(void *start, void *stop, float *ms);
+int ds41_event_record(void *event, void *stream);
 
 /* Library version string. */
 const char *ds41_gfx950_version(void);
