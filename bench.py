@@ -101,7 +101,7 @@ def main():
     bias_np = np.zeros(E, np.float32)
     wg, bias = torch.from_numpy(wg_np).to(gpu), torch.from_numpy(bias_np).to(gpu)
     y = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
-    ws = torch.empty(G.layer_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
+    ws = torch.zeros(G.layer_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
     layer_args = [G.make_layer_args(x_pool[i], wg, bias, table, 0, E, T, H, I, E, K, y, ws) for i in range(pool)]
     stream = torch.cuda.current_stream()
 
@@ -128,19 +128,20 @@ def main():
     ms_per_step = total_ms / args.steps
 
     # per-kernel durations with stage events (a separate pass over the same steps)
-    stage = G.Events(6 * args.steps)
+    NS = 6
+    stage = G.Events(NS * args.steps)
     for i in range(args.steps):
         a = layer_args[i % pool]
-        a.stage_events = stage.ptr(6 * i)
+        a.stage_events = stage.ptr(NS * i)
         G.moe_layer(a, stream)
         a.stage_events = None
     torch.cuda.synchronize()
-    names = ["router_quant", "route_plan", "gate_up_act", "down", "reduce"]
+    names = ["router", "plan", "gate_up_act", "down", "reduce"]
     stage_ms = {n: 0.0 for n in names}
     gate_bytes = down_bytes = 0
     for i in range(args.steps):
         for j, n in enumerate(names):
-            stage_ms[n] += stage.elapsed(6 * i + j, 6 * i + j + 1)
+            stage_ms[n] += stage.elapsed(NS * i + j, NS * i + j + 1)
         u = uniq[i % pool]
         gate_bytes += (u + 1) * GATE_UP_BYTES
         down_bytes += (u + 1) * DOWN_BYTES

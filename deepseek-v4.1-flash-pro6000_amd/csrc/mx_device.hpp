@@ -90,15 +90,16 @@ __device__ __forceinline__ const uint8_t *proj_scale(const ds41_device_expert &e
 
 // LDS image of the activation rows of one job: rows of `stride` bytes holding
 // E4M3 values zero-padded to a multiple of 128, and rows of `sstride` E8M0
-// scale bytes padded with 127.
+// scale bytes padded with 127 (both strides multiples of 16 bytes).
 struct XTile {
   const uint8_t *q, *s;
   int stride, sstride, tokens;
 };
 
-__device__ __forceinline__ int chunks_of(int k) { return (k + 127) >> 7; }
-__device__ __host__ __forceinline__ int xtile_stride(int k) { return ((k + 127) / 128) * 128 + 16; }
-__device__ __host__ __forceinline__ int xtile_sstride(int k) { return ((k + 127) / 128) * 4; }
+// One extra all-zero 128-k chunk (scales 127) follows the padded row, so a GEMV
+// may run whole batches past the last chunk and add exact zeros.
+__device__ __host__ __forceinline__ int xtile_stride(int k) { return ((k + 127) / 128 + 1) * 128 + 16; }
+__device__ __host__ __forceinline__ int xtile_sstride(int k) { return (((k + 127) / 128 + 1) * 4 + 15) & ~15; }
 
 // Stage `tokens` activation rows into LDS: LDS row r is source row row_idx(r) of
 // the E4M3 matrix x [*][k] and its scales xs [*][k/32]. Caller syncs.
@@ -106,7 +107,7 @@ template <class RowIdx>
 __device__ __forceinline__ void stage_xtile(uint8_t *lq, uint8_t *ls, const uint8_t *x,
                                             const uint8_t *xs, int k, int tokens, RowIdx row_idx) {
   const int stride = xtile_stride(k), sstride = xtile_sstride(k);
-  const int pieces = (stride - 16) >> 4;
+  const int pieces = (stride - 16) >> 4;  // includes the trailing zero chunk
   const bool aligned = ((((uintptr_t)x) | (uintptr_t)k) & 15u) == 0;
   for (int p = threadIdx.x; p < tokens * pieces; p += blockDim.x) {
     int r = p / pieces, off = (p - r * pieces) << 4;
@@ -129,7 +130,6 @@ __device__ __forceinline__ void stage_xtile(uint8_t *lq, uint8_t *ls, const uint
   }
 }
 
-// One wave computes out[t][row0 + j] for j < 16, t < tokens over the full K.
 // Operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950):
 //   B (fp4 weights, 128 x 16): lane l holds 32 consecutive k = 32*(l>>4) .. +31 of
 //     column l&15, low nibble first -> one 16-byte load of the weight row;
@@ -139,58 +139,101 @@ __device__ __forceinline__ void stage_xtile(uint8_t *lq, uint8_t *ls, const uint
 //   D (16 x 16 fp32): lane l holds column l&15, rows 4*(l>>4) + r in register r.
 // A = activations (tokens as rows), B = weights (channels as columns), so lane l
 // ends with channel l&15 for tokens 4*(l>>4) .. +3.
+//
+// Gemv16 streams the 16 weight rows of one wave (row l&15 at `wrow`, K bytes/2)
+// through the MFMA, 128 k per chunk. The constructor issues the first U chunk
+// loads so they are in flight while the caller stages LDS; run() then keeps two
+// register batches in flight (ping-pong, no register copies) so each wait covers
+// only the older batch. All weight loads are unconditional: lanes past the last
+// K32 group re-read a valid group and get scale 127 against zero activations,
+// and a partial last batch re-reads the last chunk without computing it.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef const u32x4 __attribute__((address_space(1))) *global_u4;
+typedef const u32x2 __attribute__((address_space(1))) *global_u2;
+
 template <int U, bool Aligned16>
-__device__ __forceinline__ v4f gemv16(const uint8_t *__restrict__ wrow, const uint8_t *__restrict__ srow,
-                                      bool row_ok, int k, const XTile &x) {
-  const int lane = threadIdx.x & 63, kb = lane >> 4, i = lane & 15;
-  const int ng = k >> 5, nch = chunks_of(k);
-  const bool a_ok = i < x.tokens;
-  const uint8_t *xa = x.q + i * x.stride + 16 * kb;
-  const uint8_t *sa = x.s + i * x.sstride + kb;
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-  uint4 b[U], nb[U];
-  uint32_t bs[U], nbs[U];
-  auto load = [&](int c0, uint4 *dst, uint32_t *dsts) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int g = 4 * (c0 + u) + kb;
-      const bool ok = row_ok && g < ng;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (ok) {
-        if (Aligned16) v = *reinterpret_cast<const uint4 *>(wrow + 16 * g);
-        else {
-          uint2 lo = *reinterpret_cast<const uint2 *>(wrow + 16 * g);
-          uint2 hi = *reinterpret_cast<const uint2 *>(wrow + 16 * g + 8);
-          v = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        }
-      }
-      dst[u] = v;
-      dsts[u] = ok ? (uint32_t)srow[g] : 127u;
+struct Gemv16 {
+  const uint8_t *w;  // weight row
+  int kb, ng, nch, nb;
+  uint4 A[U], B[U];
+
+  // 16 bytes of K32 group min(4c + kb, ng - 1) through a global-address-space
+  // pointer (global_load, counted by vmcnt only, never by lgkmcnt).
+  __device__ __forceinline__ uint4 ld(int c) const {
+    const int cc = c < nch ? c : nch - 1;
+    int g = 4 * cc + kb;
+    g = g < ng ? g : ng - 1;
+    const uint8_t *p = w + 16 * g;
+    if (Aligned16) {
+      const u32x4 v = *(global_u4)(p);
+      return make_uint4(v.x, v.y, v.z, v.w);
     }
-  };
-  load(0, b, bs);
-  for (int c0 = 0; c0 < nch; c0 += U) {
-    if (c0 + U < nch) load(c0 + U, nb, nbs);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + u;
-      if (c < nch) {
-        v8i a = {0, 0, 0, 0, 0, 0, 0, 0};
-        int as = 127;
-        if (a_ok) {
-          uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * c);
-          uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * c + 64);
-          a = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-          as = sa[4 * c];
-        }
-        v8i bv = v8i{(int)b[u].x, (int)b[u].y, (int)b[u].z, (int)b[u].w, 0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bv, acc, 0, 4, 0, as, 0, (int)bs[u]);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) { b[u] = nb[u]; bs[u] = nbs[u]; }
+    const u32x2 lo = *(global_u2)(p), hi = *(global_u2)(p + 8);
+    return make_uint4(lo.x, lo.y, hi.x, hi.y);
   }
-  return acc;
+  __device__ __forceinline__ void load(uint4 *buf, int b) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) buf[u] = ld(b * U + u);
+  }
+  __device__ __forceinline__ Gemv16(const uint8_t *wrow, int k) {
+    kb = (threadIdx.x & 63) >> 4;
+    w = wrow;
+    ng = k >> 5;
+    nch = (ng + 3) >> 2;
+    nb = (nch + U - 1) / U;
+    load(A, 0);
+  }
+  // xt: activation rows in LDS; lsw: this lane's weight-scale row in LDS (ng bytes).
+  // Chunks past the end read the zero chunk of the activation rows (exact zero
+  // products against a finite weight scale), so no MFMA sits behind a branch.
+  __device__ __forceinline__ v4f run(const XTile &xt, const uint8_t *lsw) {
+    const int lane = threadIdx.x & 63, q = lane >> 4, i = lane & 15;
+    const int ii = i < xt.tokens ? i : 0;  // padded rows repeat row 0; their outputs are dropped
+    const uint8_t *xa = xt.q + ii * xt.stride + 16 * q;
+    const uint8_t *sa = xt.s + ii * xt.sstride + q;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    auto mma = [&](const uint4 &wv, int c) {
+      const int cx = c < nch ? c : nch;  // nch is the zero chunk
+      const uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * cx);
+      const uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * cx + 64);
+      const v8i a = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      const v8i bv = v8i{(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w, 0, 0, 0, 0};
+      int g = 4 * c + kb;
+      g = g < ng ? g : ng - 1;
+      acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bv, acc, 0, 4, 0, (int)sa[4 * cx], 0, (int)lsw[g]);
+    };
+    auto compute = [&](const uint4 *buf, int b) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) mma(buf[u], b * U + u);
+    };
+    int b = 0;
+    for (; b + 2 < nb; b += 2) {
+      load(B, b + 1);
+      compute(A, b);
+      load(A, b + 2);
+      compute(B, b + 1);
+    }
+    if (b + 2 == nb) {
+      load(B, b + 1);
+      compute(A, b);
+      compute(B, b + 1);
+    } else {
+      compute(A, b);
+    }
+    return acc;
+  }
+};
+
+// Copy `bytes` contiguous bytes global -> LDS with the whole workgroup
+// (16-byte pieces when both ends allow it). Caller syncs.
+__device__ __forceinline__ void stage_bytes(uint8_t *dst, const uint8_t *src, int bytes) {
+  if (((((uintptr_t)src) | (uintptr_t)bytes) & 15u) == 0) {
+    for (int p = threadIdx.x; p < (bytes >> 4); p += blockDim.x)
+      reinterpret_cast<uint4 *>(dst)[p] = reinterpret_cast<const uint4 *>(src)[p];
+  } else {
+    for (int p = threadIdx.x; p < bytes; p += blockDim.x) dst[p] = src[p];
+  }
 }
 
 }  // namespace ds41g

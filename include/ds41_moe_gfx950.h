@@ -116,12 +116,14 @@ int ds41_router_logits(const void *x_bf16, const float *w, float *logits, int M,
 int ds41_router_topk(const float *b, int32_t *ids, int M, int N, int topk, void *stream);
 
 /* ---- fused verify MoE layer (batch.inc:220-335 bmoe + bshared) ------------- */
-/* One MoE layer for T = tokens rows, entirely on the device with no host sync:
- * router GEMV + score, top-k + route weights + route plan, MXFP8 quant,
- * fused gate/up MXFP4 GEMV + SwiGLU(limit)*w + MXFP8, down GEMV, ordered reduce
- * (ascending expert id, shared expert last). Routed experts are
- * table[expert_base + id]; the shared expert is table[shared_index]
- * (shared_index < 0: none). */
+/* One MoE layer for T = tokens rows (1..8), entirely on the device with no host
+ * sync, in five kernels: router GEMV + score + MXFP8 quant of x; top-k + route
+ * weights + route plan (one workgroup); fused gate/up MXFP4 GEMV +
+ * SwiGLU(limit)*w + MXFP8; down GEMV; ordered reduce (ascending expert id,
+ * shared expert last).
+ * Routed experts are table[expert_base + id]; the shared expert is
+ * table[shared_index] (shared_index < 0: none). hidden % 256 == 0, inter % 32 == 0.
+ * Calls that share one workspace must be ordered (same stream). */
 typedef struct ds41_moe_layer_args {
   const void *x_bf16;             /* [tokens][hidden] */
   const float *router_w;          /* [n_experts][hidden] fp32 */
@@ -139,10 +141,12 @@ typedef struct ds41_moe_layer_args {
   float *weights_out;             /* optional [tokens][topk] (device) */
   float *logits_out;              /* optional [tokens][n_experts] (device) */
   void *const *stage_events;      /* optional: 6 hipEvent_t recorded on `stream` before each of
-                                     the 5 kernels and after the last (for per-kernel timing) */
+                                     the 5 kernels (router, plan, gate/up/act, down, reduce) and
+                                     after the last, for per-kernel timing */
 } ds41_moe_layer_args;
 size_t ds41_moe_layer_workspace_bytes(int tokens, int hidden, int inter, int n_experts,
                                       int topk);
+
 int ds41_moe_verify_layer(const ds41_moe_layer_args *args, void *stream);
 /* Reads the route plan of the last layer call from its workspace (host copy, synchronous):
  * unique expert count and ids; returns the count or -1. */

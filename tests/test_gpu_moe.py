@@ -235,7 +235,7 @@ def test_moe_layer_vs_oracle(gpu):
     bias_np = np.zeros(E, np.float32)
     x, wg, bias = dev(x_np, gpu), dev(wg_np, gpu), dev(bias_np, gpu)
     y = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
-    ws = torch.empty(G.layer_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
+    ws = torch.zeros(G.layer_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
     ids = torch.empty((T, K), dtype=torch.int32, device=gpu)
     wts = torch.empty((T, K), dtype=torch.float32, device=gpu)
     logits = torch.empty((T, E), dtype=torch.float32, device=gpu)
