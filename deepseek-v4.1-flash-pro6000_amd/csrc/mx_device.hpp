@@ -159,7 +159,9 @@ struct Gemv16 {
   uint4 A[U], B[U];
 
   // 16 bytes of K32 group min(4c + kb, ng - 1) through a global-address-space
-  // pointer (global_load, counted by vmcnt only, never by lgkmcnt).
+  // pointer (global_load, counted by vmcnt only, never by lgkmcnt). Plain (not
+  // non-temporal) loads: each 128-byte row line is consumed by two consecutive
+  // chunk loads, and the second one must still find the line in L2.
   __device__ __forceinline__ uint4 ld(int c) const {
     const int cc = c < nch ? c : nch - 1;
     int g = 4 * cc + kb;
