@@ -2,3 +2,4 @@
 // file-scope device status word without relocatable device code.
 #include "moe_kernels.inc"
 #include "moe_layer.inc"
+#include "accept.inc"

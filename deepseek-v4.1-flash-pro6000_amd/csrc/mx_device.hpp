@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "ds41_moe_gfx950.h"
+#include "ds41_accept_gfx950.h"
 
 namespace ds41g {
 

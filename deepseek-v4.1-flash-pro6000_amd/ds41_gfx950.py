@@ -63,6 +63,11 @@ def lib():
         _lib = ctypes.CDLL(LIB_PATH)
         _lib.ds41_moe_layer_workspace_bytes.restype = ctypes.c_size_t
         _lib.ds41_gfx950_version.restype = ctypes.c_char_p
+        _lib.ds41_spark_accept_workspace_bytes.restype = ctypes.c_size_t
+        _lib.ds41_spark_verify_logits_gpu_v2.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_double,
+            ctypes.c_double, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+            ctypes.c_int, ctypes.c_void_p]
     return _lib
 
 
@@ -254,6 +259,39 @@ class Events:
             lib().ds41_events_destroy(self.arr, self.n)
         except Exception:
             pass
+
+
+# ---- acceptance ------------------------------------------------------------------
+def accept_workspace(drafts, vocab, device="cuda"):
+    import torch
+    return torch.zeros(lib().ds41_spark_accept_workspace_bytes(drafts, vocab), dtype=torch.uint8, device=device)
+
+
+def verify_logits(target, draft, drafts_dev, temperature, top_p, seed, step, out, workspace, flags=0, stream=None):
+    """target [k+1][V] fp32, draft [k][V] fp32 (None when greedy), drafts_dev int32 [k],
+    out: device tensor of >= 40 bytes receiving ds41_spark_result."""
+    k = target.shape[0] - 1
+    V = target.shape[1]
+    check(lib().ds41_spark_verify_logits_gpu_v2(
+        target.data_ptr(), 0 if draft is None else draft.data_ptr(), 0 if k == 0 else drafts_dev.data_ptr(), k, V,
+        float(temperature), float(top_p), seed, step, out.data_ptr(), workspace.data_ptr(), workspace.numel(),
+        flags, _stream(stream).value), "ds41_spark_verify_logits_gpu_v2")
+
+
+def result_tuple(buf):
+    """Host view of a ds41_spark_result held in a device/host tensor."""
+    import numpy as np
+    raw = buf.cpu().numpy().view(np.int32)
+    emitted = int(raw[6])
+    return (tuple(int(v) for v in raw[:max(emitted, 0)]), int(raw[7]), int(raw[8]), int(raw[9])) if emitted >= 0 \
+        else ((), -1, -1, -1)
+
+
+def accept_fallbacks(workspace, drafts, vocab):
+    v = ctypes.c_uint32(0)
+    check(lib().ds41_spark_accept_fallbacks(ctypes.c_void_p(workspace.data_ptr()), drafts, vocab, ctypes.byref(v)),
+          "ds41_spark_accept_fallbacks")
+    return v.value
 
 
 def layer_plan(workspace, T, H, I, E, K):

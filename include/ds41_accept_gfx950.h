@@ -1,0 +1,49 @@
+/*
+ * ds41 speculative-decode acceptance sampler for MI355X (gfx950): C ABI.
+ *
+ * GPU replacement of the host fp64 accept step the engine runs after verify
+ * (engine/src/speculation.cpp:179-182 -> engine/src/sampling.cpp:142-275 ->
+ * engine/third_party/spark/src/sampling.cpp:30-56 ds41_spark_probabilities +
+ * ds41_spark_verify_v2). All pointers are device memory; `stream` is a
+ * hipStream_t passed as void*; returns a hipError_t value as int.
+ */
+#ifndef DS41_ACCEPT_GFX950_H
+#define DS41_ACCEPT_GFX950_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* engine/third_party/spark/include/ds41/spark.h ds41_spark_result. emitted == -1
+ * marks an invalid input (non-finite logits, draft id out of range, q[d] == 0),
+ * where the host sampler throws. */
+typedef struct ds41_spark_result {
+  int32_t tokens[6];
+  int emitted, accepted_drafts, accepted_input_rows, rejected;
+} ds41_spark_result;
+
+/* Device workspace for ds41_spark_verify_logits_gpu_v2 (drafts <= 5). */
+size_t ds41_spark_accept_workspace_bytes(int drafts, int vocab);
+
+/* The whole accept step from fp32 logits: probabilities of every target row
+ * [drafts+1][vocab] and draft row [drafts][vocab] with temperature floor
+ * max(T, 1e-5) (T == 0: greedy, draft_logits may be NULL), then verify_v2 with
+ * Philox v2 uniforms (seed, step). Decisions and tokens equal the host
+ * sampler's: a decision whose margin is within the bound on the difference
+ * between parallel and sequential fp64 sums is recomputed with sequential sums.
+ * flags bit 0 forces that sequential path for every decision (testing).
+ * top_p < 1 with T > 0 returns hipErrorNotSupported in this version. */
+int ds41_spark_verify_logits_gpu_v2(const float *target_logits, const float *draft_logits,
+                                    const int32_t *drafts_dev, int drafts, int vocab,
+                                    double temperature, double top_p, uint64_t seed, uint64_t step,
+                                    ds41_spark_result *out, void *workspace, size_t workspace_bytes,
+                                    int flags, void *stream);
+/* Number of accept steps that took the sequential path since the workspace was
+ * zeroed (synchronous read). */
+int ds41_spark_accept_fallbacks(const void *workspace, int drafts, int vocab, uint32_t *count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
