@@ -61,6 +61,79 @@ def cpu_baseline(x_np, wg_np, bias_np, experts_gpu, H, I, E, seconds):
                       f"shared) of the C oracle, {per * 1e3:.1f} ms each"}
 
 
+def bench_accept(gpu, steps, cpu_seconds, no_cpu):
+    """acceptance alone, k=3 drafts + 1 bonus over V=129280, T=1.0, top-p 1.0, Philox-seeded,
+    `steps` consecutive steps over a pool of 16 resident logit sets (target N(0, 2.5^2), draft = target +
+    N(0, 0.5^2)); drafts sampled from q (slot k, purpose Draft) as the drafter does."""
+    import numpy as np
+    import torch
+    import ds41_gfx950 as G
+    import oracle as O
+    k, V, pool, seed = 3, 129280, 16, 0
+    rng = np.random.default_rng(2)
+    tgt, drf, ids = [], [], []
+    for i in range(pool):
+        t = (rng.standard_normal((k + 1, V)) * 2.5).astype(np.float32)
+        d = (t[:k] + rng.standard_normal((k, V)) * 0.5).astype(np.float32)
+        q = [O.probabilities(d[j], 1.0, 1.0) for j in range(k)]
+        ids.append([O.sample_v2(q[j], seed, i, j, 1) for j in range(k)])
+        tgt.append(t)
+        drf.append(d)
+    T_dev = torch.from_numpy(np.stack(tgt)).to(gpu)
+    D_dev = torch.from_numpy(np.stack(drf)).to(gpu)
+    I_dev = torch.tensor(ids, dtype=torch.int32, device=gpu)
+    ws = G.accept_workspace(k, V, gpu)
+    out = torch.zeros((steps, 16), dtype=torch.int32, device=gpu)
+    stream = torch.cuda.current_stream()
+    for s in range(50):
+        G.verify_logits(T_dev[s % pool], D_dev[s % pool], I_dev[s % pool], 1.0, 1.0, seed, s, out[s], ws)
+    ev = G.Events(2)
+    torch.cuda.synchronize()
+    ev.record(0, stream)
+    for s in range(steps):
+        G.verify_logits(T_dev[s % pool], D_dev[s % pool], I_dev[s % pool], 1.0, 1.0, seed, s, out[s], ws)
+    ev.record(1, stream)
+    torch.cuda.synchronize()
+    us = ev.elapsed(0, 1) * 1e3 / steps
+    res = out.cpu().numpy()
+    accepted = float(np.mean(res[:, 7]))
+    # parity spot check of the timed results against the oracle (every 500th step)
+    for s in range(0, steps, 500):
+        ref = O.accept_logits(tgt[s % pool], drf[s % pool], np.array(ids[s % pool], np.int32), 1.0, 1.0, seed, s)
+        if G.result_tuple(out[s]) != ref.as_tuple():
+            raise AssertionError(f"accept parity failed at step {s}")
+    cpu = None
+    if not no_cpu:
+        R = O.ref()
+        kind = "reference" if R is not None else "port"
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds:
+            s = n
+            x = tgt[s % pool]
+            if R is not None:  # the reference's own host sampler (compiled from its sources)
+                import ctypes
+                p = np.empty((k + 1, V), np.float64)
+                q = np.empty((k, V), np.float64)
+                for j in range(k):
+                    R.ds41_spark_probabilities(drf[s % pool][j].ctypes.data, q[j].ctypes.data, V, 1.0, 1.0)
+                for j in range(k + 1):
+                    R.ds41_spark_probabilities(x[j].ctypes.data, p[j].ctypes.data, V, 1.0, 1.0)
+                d = np.array(ids[s % pool], np.int32)
+                r = O.SparkResult()
+                R.ds41_spark_verify_v2(d.ctypes.data, q.ctypes.data, p.ctypes.data, k, V, 0, seed, s,
+                                       ctypes.byref(r))
+            else:
+                O.accept_logits(x, drf[s % pool], np.array(ids[s % pool], np.int32), 1.0, 1.0, seed, s)
+            n += 1
+        per = (time.perf_counter() - t0) / n
+        cpu = {"value": per * 1e6, "unit": "us/step", "cores": 1, "kind": kind,
+               "sample": f"{n} accept steps (7 fp64 probability rows of V={V} + verify_v2), single thread"}
+    return {"workload": "configs[2]: accept k=3 + bonus, V=129280, T=1.0, top-p 1.0", "steps": steps,
+            "us_per_step": us, "mean_accepted_drafts": accepted,
+            "sequential_path_steps": G.accept_fallbacks(ws, k, V),
+            "bytes_per_step": 7 * V * 4, "cpu_baseline": cpu}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -68,6 +141,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--accept-steps", type=int, default=10000)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the verify path "
@@ -160,6 +234,12 @@ def main():
         cpu = cpu_baseline(x_pool_np[0], wg_np, bias_np, experts, H, I, E, args.cpu_seconds)
         log(f"cpu baseline: {cpu}")
 
+    accept = bench_accept(gpu, args.accept_steps, min(args.cpu_seconds, 10.0), args.no_cpu) \
+        if args.accept_steps > 0 else None
+    if accept:
+        log(f"accept: {accept['us_per_step']:.1f} us/step, mean accepted drafts {accept['mean_accepted_drafts']:.2f}, "
+            f"cpu {accept['cpu_baseline']}")
+
     out = {
         "metric": METRIC, "value": T / (ms_per_step * 1e-3), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
@@ -174,6 +254,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "layer_gate_up_act_kernel", "achieved": gate_gbps,
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": gate_gbps / PEAK_HBM_GBPS, "traffic": None},
         "cpu_baseline": cpu,
+        "accept": accept,
     }
     print(json.dumps(out), flush=True)
 
