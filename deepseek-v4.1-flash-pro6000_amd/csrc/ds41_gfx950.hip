@@ -2,4 +2,5 @@
 // file-scope device status word without relocatable device code.
 #include "moe_kernels.inc"
 #include "moe_layer.inc"
+#include "verify_stack.inc"
 #include "accept.inc"

@@ -45,7 +45,32 @@ class MoeLayerArgs(ctypes.Structure):
                 ("stage_events", ctypes.c_void_p)]
 
 
+class ExpertLayout(ctypes.Structure):
+    _fields_ = [("offset", ctypes.c_uint64 * 6), ("bytes", ctypes.c_uint64)]
+
+
+class StackLayer(ctypes.Structure):
+    _fields_ = [("router_w", ctypes.c_void_p), ("router_bias", ctypes.c_void_p), ("table", ctypes.c_void_p),
+                ("expert_base", ctypes.c_int32), ("shared_index", ctypes.c_int32),
+                ("host_index", ctypes.c_void_p), ("host_slabs", ctypes.c_void_p),
+                ("host_slab_count", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class StackDesc(ctypes.Structure):
+    _fields_ = [("layers", ctypes.c_int32), ("max_tokens", ctypes.c_int32), ("hidden", ctypes.c_int32),
+                ("inter", ctypes.c_int32), ("n_experts", ctypes.c_int32), ("topk", ctypes.c_int32),
+                ("score_mode", ctypes.c_int32), ("route_scale", ctypes.c_float), ("swiglu_limit", ctypes.c_float),
+                ("layer", ctypes.POINTER(StackLayer))]
+
+
+class StackStats(ctypes.Structure):
+    _fields_ = [("steps", ctypes.c_uint64), ("layers", ctypes.c_uint64), ("resident_routed", ctypes.c_uint64),
+                ("host_fetched", ctypes.c_uint64), ("h2d_bytes", ctypes.c_uint64),
+                ("invalid_layers", ctypes.c_uint64)]
+
+
 assert ctypes.sizeof(DeviceExpert) == 64 and ctypes.sizeof(GemmJob) == 32
+assert ctypes.sizeof(StackLayer) == 56 and ctypes.sizeof(ExpertLayout) == 56
 
 
 class SparkResult(ctypes.Structure):
@@ -300,3 +325,91 @@ def layer_plan(workspace, T, H, I, E, K):
     if n < 0:
         raise RuntimeError("ds41_moe_layer_plan failed")
     return list(ids[:n])
+
+
+# ---- verify step through a layer stack with a host expert tier ----------------------
+def slab_layout(hidden, inter):
+    """Canonical expert slab: ([gate, gate_scale, up, up_scale, down, down_scale] byte offsets, slab bytes)."""
+    out = ExpertLayout()
+    check(lib().ds41_expert_slab_layout(hidden, inter, ctypes.byref(out)), "ds41_expert_slab_layout")
+    return list(out.offset), int(out.bytes)
+
+
+SLAB_FIELDS = ("gate", "gate_scale", "up", "up_scale", "down", "down_scale")
+
+
+def slab_entry(base_ptr, offsets, slot=-1):
+    """DeviceExpert pointing into a canonical slab at base_ptr."""
+    e = DeviceExpert()
+    for f, o in zip(SLAB_FIELDS, offsets):
+        setattr(e, f, base_ptr + o)
+    e.ready, e.generation, e.slot = 0, 0, slot
+    return e
+
+
+class HostSlabs:
+    """Pinned host memory from ds41_host_alloc (hipHostMalloc) viewed as a uint8 CPU tensor of
+    [count][slab] bytes; freed with the object."""
+
+    def __init__(self, count, slab):
+        import numpy as np
+        import torch
+        self.ptr = ctypes.c_void_p(0)
+        check(lib().ds41_host_alloc(ctypes.c_size_t(count * slab), ctypes.byref(self.ptr)), "ds41_host_alloc")
+        buf = (ctypes.c_uint8 * (count * slab)).from_address(self.ptr.value)
+        self.tensor = torch.from_numpy(np.ctypeslib.as_array(buf).reshape(count, slab))
+
+    def __del__(self):
+        try:
+            if self.ptr.value:
+                self.tensor = None
+                lib().ds41_host_free(self.ptr)
+                self.ptr = ctypes.c_void_p(0)
+        except Exception:
+            pass
+
+
+class VerifyStack:
+    """ds41_verify_stack_*: layers is a list of dicts with router_w, router_bias, table (device tensors),
+    expert_base, shared_index and optionally host_index (device int32 [E]) + host_slabs (pinned uint8
+    tensor of host_slab_count slabs). The tensors must outlive the stack."""
+
+    def __init__(self, layers, max_tokens, hidden, inter, n_experts, topk, score_mode=0, route_scale=1.5,
+                 swiglu_limit=10.0, slab_bytes=None):
+        arr = (StackLayer * len(layers))()
+        for i, d in enumerate(layers):
+            arr[i].router_w, arr[i].router_bias = d["router_w"].data_ptr(), d["router_bias"].data_ptr()
+            arr[i].table = d["table"].data_ptr()
+            arr[i].expert_base, arr[i].shared_index = d.get("expert_base", 0), d.get("shared_index", -1)
+            hi, hs = d.get("host_index"), d.get("host_slabs")
+            arr[i].host_index = 0 if hi is None else hi.data_ptr()
+            arr[i].host_slabs = 0 if hs is None else hs.data_ptr()
+            arr[i].host_slab_count = 0 if hs is None else hs.numel() // slab_bytes
+        self._arr = arr
+        desc = StackDesc(len(layers), max_tokens, hidden, inter, n_experts, topk, score_mode, route_scale,
+                         swiglu_limit, arr)
+        self.handle = ctypes.c_void_p(0)
+        check(lib().ds41_verify_stack_create(ctypes.byref(desc), ctypes.byref(self.handle)),
+              "ds41_verify_stack_create")
+        self.L, self.H, self.K = len(layers), hidden, topk
+
+    def step(self, x, y, route_ids=None, layer_out=None, ids_out=None, weights_out=None, stream=None):
+        T = x.shape[0]
+        check(lib().ds41_verify_stack_step(self.handle, _p(x), _p(y), T, _p(route_ids), _p(layer_out), _p(ids_out),
+                                           _p(weights_out), _stream(stream)), "ds41_verify_stack_step")
+
+    def stats(self):
+        st = StackStats()
+        check(lib().ds41_verify_stack_stats(self.handle, ctypes.byref(st)), "ds41_verify_stack_stats")
+        return {f: int(getattr(st, f)) for f, _ in StackStats._fields_}
+
+    def close(self):
+        if self.handle:
+            lib().ds41_verify_stack_destroy(self.handle)
+            self.handle = ctypes.c_void_p(0)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

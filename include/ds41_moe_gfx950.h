@@ -122,7 +122,8 @@ int ds41_router_topk(const float *b, int32_t *ids, int M, int N, int topk, void 
  * SwiGLU(limit)*w + MXFP8; down GEMV; ordered reduce (ascending expert id,
  * shared expert last).
  * Routed experts are table[expert_base + id]; the shared expert is
- * table[shared_index] (shared_index < 0: none). hidden % 256 == 0, inter % 32 == 0.
+ * table[shared_index] (shared_index < 0: none). hidden % 256 == 0 (<= 8192),
+ * inter % 32 == 0, n_experts <= 512, topk <= 8.
  * Calls that share one workspace must be ordered (same stream). */
 typedef struct ds41_moe_layer_args {
   const void *x_bf16;             /* [tokens][hidden] */
@@ -152,6 +153,83 @@ int ds41_moe_verify_layer(const ds41_moe_layer_args *args, void *stream);
  * unique expert count and ids; returns the count or -1. */
 int ds41_moe_layer_plan(const void *workspace, int tokens, int hidden, int inter, int n_experts,
                         int topk, int32_t *unique_ids, int max_ids);
+
+/* ---- verify step through a stack of MoE layers with a host expert tier ------ */
+/* Canonical expert slab (the reference's 18.8 MB offload slot, store.hpp:32-37,
+ * offload.cpp:443-457): gate W [inter][hidden/2] | gate scales [inter][hidden/32]
+ * | up W | up scales | down W [hidden][inter/2] | down scales [hidden][inter/32],
+ * each tensor 256-byte aligned; `bytes` is the slab size (4 KiB multiple).
+ * Returns 0, or hipErrorInvalidValue for hidden/inter not multiples of 32. */
+typedef struct ds41_expert_layout {
+  uint64_t offset[6];
+  uint64_t bytes;
+} ds41_expert_layout;
+int ds41_expert_slab_layout(int hidden, int inter, ds41_expert_layout *out);
+
+/* One layer of the stack. Routed expert id e is table[expert_base + e]; the
+ * shared expert is table[shared_index] (< 0: none). Residency (the reference's
+ * OffloadStore placement, components/moe/src/offload.cpp:240-381): host_index (device int32
+ * [n_experts]) is -1 for an HBM-resident expert and otherwise the index of the
+ * expert's canonical slab in host_slabs (pinned host memory from hipHostMalloc,
+ * host_slab_count slabs), whose table entry is then never read.
+ * host_index == NULL: all resident. */
+typedef struct ds41_stack_layer {
+  const float *router_w;           /* device fp32 [n_experts][hidden] */
+  const float *router_bias;        /* device fp32 [n_experts] */
+  const ds41_device_expert *table; /* device */
+  int32_t expert_base, shared_index;
+  const int32_t *host_index;       /* device, nullable */
+  const uint8_t *host_slabs;       /* pinned host, nullable when host_index is NULL */
+  int32_t host_slab_count;
+  int32_t reserved;
+} ds41_stack_layer;
+
+typedef struct ds41_stack_desc {
+  int32_t layers, max_tokens, hidden, inter, n_experts, topk, score_mode;
+  float route_scale, swiglu_limit;
+  const ds41_stack_layer *layer;   /* host array [layers], copied at create */
+} ds41_stack_desc;
+
+/* Cumulative counters of the layers that have a host tier (read back each layer). */
+typedef struct ds41_stack_stats {
+  uint64_t steps, layers;          /* layers = layer passes with a host tier */
+  uint64_t resident_routed;        /* routed experts served from HBM (shared excluded) */
+  uint64_t host_fetched;           /* host-tier experts copied in */
+  uint64_t h2d_bytes;
+  uint64_t invalid_layers;         /* layer passes whose routes were rejected */
+} ds41_stack_stats;
+
+/* Creates a stack (allocates: the layer workspace, max_tokens*topk staging
+ * slots, two activation buffers, a pinned plan read-back buffer, a copy stream
+ * at default priority and two events, on the current device). *stack receives
+ * an opaque handle. The verify-step counterpart of the MoE part of the
+ * reference's Forward::verify (engine/src/forward.cu:769, batched through
+ * engine/src/hotpath/batch.inc:220-335), with OffloadStore::order/upload
+ * (components/moe/src/offload.cpp:443-457) as the host tier. */
+int ds41_verify_stack_create(const ds41_stack_desc *desc, void **stack);
+/* One verify step of `tokens` rows (1..max_tokens) through every layer: layer l
+ * takes layer l-1's output (layer 0 takes x). Per layer: router + plan on
+ * `stream`; a read-back of the plan (one host wait per layer that has a host
+ * tier, as the reference's per-layer route-event wait, batch.inc:224); resident gate/up and
+ * down run while the host issues hipMemcpyAsync of the routed host-tier slabs
+ * on the copy stream into staging slots; host-tier gate/up and down wait on the
+ * copies' event; then the ordered reduce.
+ * route_ids: nullable device int32 [layers][tokens][topk] that replaces the
+ * router's top-k (the weights still come from the router's scores).
+ * layer_out (nullable, device bf16 [layers][tokens][hidden]): every layer's
+ * output; ids_out / weights_out (nullable, device [layers][tokens][topk]).
+ * Steps on one stack must not overlap (one workspace and staging area). */
+int ds41_verify_stack_step(void *stack, const void *x_bf16, void *y_bf16, int tokens,
+                           const int32_t *route_ids, void *layer_out, int32_t *ids_out,
+                           float *weights_out, void *stream);
+int ds41_verify_stack_stats(void *stack, ds41_stack_stats *out);
+int ds41_verify_stack_destroy(void *stack);
+/* Pinned host memory for host-tier slabs (the reference's HostBuffer,
+ * components/moe/include/ds41/store.hpp:161-174, which registers an existing
+ * mapping; here the pages are allocated pinned with hipHostMalloc, so DMA
+ * copies from them run asynchronously). Synchronous; *out is NULL on error. */
+int ds41_host_alloc(size_t bytes, void **out);
+int ds41_host_free(void *p);
 
 /* MXFP4 dequantisation: w [n][k/2] + s [n][k/32] -> fp32 [n][k] (bit-exact). */
 int ds41_dequant_mxfp4(const uint8_t *w, const uint8_t *s, float *out, int n, int k,

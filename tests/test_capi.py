@@ -46,3 +46,28 @@ def test_abi_struct_sizes():
     # argument validation happens on the host, before any device call
     assert lib.ds41_quantize_mxfp8(None, None, None, 1, 32, None) == 1
     assert lib.ds41_grouped_mxfp4(None, None, 1, 0, 8, 32, None) == 1
+
+
+def test_stack_abi_host_checks():
+    """Layout of the expert slab and the stack descriptors; argument checks that run before any device call."""
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "deepseek-v4.1-flash-pro6000_amd"))
+    import ds41_gfx950 as G
+    assert ctypes.sizeof(G.StackLayer) == 56 and ctypes.sizeof(G.StackStats) == 48
+    off, slab = G.slab_layout(4096, 2880)
+    # the reference's offload slot: 18,800,640 B per expert (gate/up/down weights + e8m0 scales)
+    assert slab == 18800640 and off == [0, 5898240, 6266880, 12165120, 12533760, 18432000]
+    assert all(o % 256 == 0 for o in off) and slab % 4096 == 0
+    with pytest.raises(RuntimeError):
+        G.slab_layout(4096, 2881)
+    lib = ctypes.CDLL(LIB)
+    h = ctypes.c_void_p(0)
+    layers = (G.StackLayer * 1)()
+    desc = G.StackDesc(1, 4, 4096, 2880, 384, 6, 0, 1.5, 10.0, layers)  # null router/table pointers
+    assert lib.ds41_verify_stack_create(ctypes.byref(desc), ctypes.byref(h)) == 1 and not h.value
+    desc = G.StackDesc(1, 9, 4096, 2880, 384, 6, 0, 1.5, 10.0, layers)  # 9 tokens > 8
+    assert lib.ds41_verify_stack_create(ctypes.byref(desc), ctypes.byref(h)) == 1
+    desc = G.StackDesc(1, 4, 4096, 2880, 513, 6, 0, 1.5, 10.0, layers)  # > 512 experts
+    assert lib.ds41_verify_stack_create(ctypes.byref(desc), ctypes.byref(h)) == 1
+    assert lib.ds41_verify_stack_step(None, None, None, 1, None, None, None, None, None) == 1
+    assert lib.ds41_verify_stack_destroy(None) == 1
