@@ -258,7 +258,18 @@ def main():
     ap.add_argument("--accept-steps", type=int, default=10000)
     ap.add_argument("--stack-steps", type=int, default=1000)
     ap.add_argument("--stack-warmup", type=int, default=20)
+    ap.add_argument("--copy-probe", type=int, default=0,
+                    help="only run 5 plain device copies of this many bytes (HBM counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+        src = torch.ones(args.copy_probe, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 5 x {args.copy_probe} B device-to-device copies done")
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the verify path "
               "is a single-GPU workload here and multi-GPU sharding is design-only.", file=sys.stderr)

@@ -398,6 +398,10 @@ class VerifyStack:
         check(lib().ds41_verify_stack_step(self.handle, _p(x), _p(y), T, _p(route_ids), _p(layer_out), _p(ids_out),
                                            _p(weights_out), _stream(stream)), "ds41_verify_stack_step")
 
+    def layer(self, l, x, y, route_ids=None, ids_out=None, weights_out=None, stream=None):
+        check(lib().ds41_verify_stack_layer(self.handle, l, _p(x), _p(y), x.shape[0], _p(route_ids), _p(ids_out),
+                                            _p(weights_out), _stream(stream)), "ds41_verify_stack_layer")
+
     def stats(self):
         st = StackStats()
         check(lib().ds41_verify_stack_stats(self.handle, ctypes.byref(st)), "ds41_verify_stack_stats")

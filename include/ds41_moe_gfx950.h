@@ -222,6 +222,14 @@ int ds41_verify_stack_create(const ds41_stack_desc *desc, void **stack);
 int ds41_verify_stack_step(void *stack, const void *x_bf16, void *y_bf16, int tokens,
                            const int32_t *route_ids, void *layer_out, int32_t *ids_out,
                            float *weights_out, void *stream);
+/* One layer of the same step (layer 0..layers-1), for hosts that run other
+ * work (attention) between MoE layers: x [tokens][hidden] -> y, route_ids /
+ * ids_out / weights_out [tokens][topk] (nullable). y may alias x (x is read
+ * only by the layer's first kernel).
+ * The per-layer entry of the reference's bmoe (engine/src/hotpath/batch.inc:220). */
+int ds41_verify_stack_layer(void *stack, int layer, const void *x_bf16, void *y_bf16, int tokens,
+                            const int32_t *route_ids, int32_t *ids_out, float *weights_out,
+                            void *stream);
 int ds41_verify_stack_stats(void *stack, ds41_stack_stats *out);
 int ds41_verify_stack_destroy(void *stack);
 /* Pinned host memory for host-tier slabs (the reference's HostBuffer,

@@ -200,3 +200,20 @@ def test_stack_invalid_route_ids_give_nan(gpu):
     assert st.tier.stats()["invalid_layers"] - before["invalid_layers"] == 1
     ok = st.run("tier", x)  # the stack recovers on the next step
     check_same(ok, st.run("all", x))
+
+
+def test_stack_layer_entry_matches_step(gpu):
+    """ds41_verify_stack_layer called layer by layer (as an engine with attention in between would)
+    gives the step's bytes; y aliasing x is allowed."""
+    import torch
+    L, H, I, E, K, T = 3, 512, 256, 32, 6, 3
+    st = Stack(gpu, 26, L, H, I, E, K, 4, [range(l, E, 5) for l in range(L)])
+    x = rand_x(gpu, 11, T, H)
+    y, lo, ids, w = st.run("tier", x)
+    cur = x.clone()
+    for l in range(L):
+        i = torch.empty((T, K), dtype=torch.int32, device=gpu)
+        st.tier.layer(l, cur, cur, ids_out=i)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(i), ids[l])
+        assert np.array_equal(host(cur).view(np.uint8), (y if l == L - 1 else lo[l]).view(np.uint8))
