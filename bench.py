@@ -26,6 +26,10 @@ EXPERT_BYTES = 18_800_640          # gate + up + down weights and E8M0 scales (H
 GATE_UP_BYTES = 2 * (2880 * 2048 + 2880 * 128)
 DOWN_BYTES = 4096 * 1440 + 4096 * 90
 PEAK_HBM_GBPS = 8000.0
+# HBM bytes per gate/up/act launch from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0), calibrated
+# on a plain 1 GiB device copy, at mean U = 23.328 routed experts + shared
+# (profiles/verify_layer_config1_traffic.md); the algorithmic figure at that U is 304,923,000 B.
+GATE_UP_TRAFFIC_BYTES = 305_702_000
 METRIC = "verify tokens/s per MTP step (T=1+k); MoE HBM GB/s as % of 8 TB/s peak"
 
 
@@ -383,7 +387,8 @@ def main():
         "hbm_gbps": layer_gbps, "hbm_frac": layer_gbps / PEAK_HBM_GBPS,
         "stage_us": {n: avg[n] * 1e3 for n in names},
         "roofline": {"bound": "hbm", "kernel": "layer_gate_up_act_kernel", "achieved": gate_gbps,
-                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": gate_gbps / PEAK_HBM_GBPS, "traffic": None},
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": gate_gbps / PEAK_HBM_GBPS, "traffic": GATE_UP_TRAFFIC_BYTES,
+                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, calibrated)"},
         "cpu_baseline": cpu,
         "accept": accept,
         "step40": stack,

@@ -262,3 +262,33 @@ def test_moe_layer_vs_oracle(gpu):
     err = rel_l2(O.bf16_to_f32(gy), O.bf16_to_f32(ref_y))
     say(f"  unique experts {len(routed)}, y rel-L2 {err:.3e}, bf16 exact {np.mean(gy == ref_y):.4f}")
     assert err <= 1e-3
+
+
+def test_moe_layer_topk_ties_lower_id_first(gpu):
+    """Eight experts with bit-identical router rows (identical scores) lead every token: the planner's
+    top-6 must be the six lowest of them in ascending id (ties -> lower id, batch.inc:228-237)."""
+    import torch
+    import ds41_gfx950 as G
+    H, I, E, K, T = 512, 256, 64, 6, 4
+    P, experts = make_layer(gpu, 13, H, I, E, T)
+    table, _ = G.device_table(experts, gpu)
+    rng = np.random.default_rng(14)
+    row = rand_x(rng, 1, H)
+    x_np = np.repeat(row, T, axis=0)
+    wg_np = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    tied = [2, 5, 9, 30, 31, 47, 50, 63]
+    lead = (0.05 * np.sign(O.bf16_to_f32(row[0]))).astype(np.float32)
+    wg_np[tied] = lead
+    bias_np = np.zeros(E, np.float32)
+    x, wg, bias = dev(x_np, gpu), dev(wg_np, gpu), dev(bias_np, gpu)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(G.layer_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
+    ids = torch.empty((T, K), dtype=torch.int32, device=gpu)
+    logits = torch.empty((T, E), dtype=torch.float32, device=gpu)
+    G.moe_layer(G.make_layer_args(x, wg, bias, table, 0, E, T, H, I, E, K, y, ws, ids_out=ids, logits_out=logits))
+    torch.cuda.synchronize()
+    lg = host(logits)
+    assert np.all(lg[:, tied] == lg[:, tied[:1]])  # identical rows give identical scores
+    u, b = O.router_scores(lg, bias_np)
+    assert np.array_equal(host(ids), O.topk(b, K))
+    assert np.array_equal(host(ids), np.tile(np.array(tied[:K], np.int32), (T, 1)))
