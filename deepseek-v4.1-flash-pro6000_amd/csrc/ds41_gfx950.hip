@@ -2,5 +2,6 @@
 // file-scope device status word without relocatable device code.
 #include "moe_kernels.inc"
 #include "moe_layer.inc"
+#include "prefill.inc"
 #include "verify_stack.inc"
 #include "accept.inc"

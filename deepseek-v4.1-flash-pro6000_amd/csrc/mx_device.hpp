@@ -102,33 +102,72 @@ struct XTile {
 __device__ __host__ __forceinline__ int xtile_stride(int k) { return ((k + 127) / 128 + 1) * 128 + 16; }
 __device__ __host__ __forceinline__ int xtile_sstride(int k) { return (((k + 127) / 128 + 1) * 4 + 15) & ~15; }
 
+// Byte mask (0xff per byte) of the E4M3 bytes whose exponent field is >= 7 (|v| >= 1).
+__device__ __forceinline__ uint32_t e4m3_big_mask(uint32_t v) {
+  const uint32_t t = (((v >> 3) & 0x0f0f0f0fu) + 0x09090909u) & 0x10101010u;
+  return (t >> 4) * 0xffu;
+}
+
+// Magnitude split of the activation rows. The scaled MFMA forms each K32 block
+// dot with a window of about 14 bits below the block's largest product
+// (measured on gfx950: with a 2688 product in the block a lone 2^-4 product is
+// dropped, 2^-3 kept), so MXFP8 rows, whose largest byte in every block has
+// exponent field 14 or 15, lose their smallest products. Split, a row becomes
+// two rows: its bytes with |v| >= 1 and its bytes with |v| < 1; each half fits
+// the window, and the two results are added in fp32. With T <= 8 tokens the
+// halves fill rows 0..T4-1 and T4..2*T4-1 (T4 = T rounded up to 4) of the
+// 16-row MFMA, so the split costs no extra MFMA: split_combine() adds each
+// token's two rows, which sit 4*T4 lanes apart.
+__device__ __host__ __forceinline__ int split_rows(int tokens) { return 2 * ((tokens + 3) & ~3); }
+__device__ __forceinline__ v4f split_combine(v4f acc, int tokens) {
+  const int shift = 4 * ((tokens + 3) & ~3);
+  v4f o;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) o[r] = acc[r] + __shfl_down(acc[r], shift);
+  return o;
+}
+
 // Stage `tokens` activation rows into LDS: LDS row r is source row row_idx(r) of
-// the E4M3 matrix x [*][k] and its scales xs [*][k/32]. Caller syncs.
-template <class RowIdx>
-__device__ __forceinline__ void stage_xtile(uint8_t *lq, uint8_t *ls, const uint8_t *x,
-                                            const uint8_t *xs, int k, int tokens, RowIdx row_idx) {
+// the E4M3 matrix x [*][k] and its scales xs [*][k/32]; with Split, the
+// split_rows(tokens) rows described above (padding rows zero, scale 127).
+// Returns the number of LDS rows. Caller syncs.
+template <bool Split = false, class RowIdx>
+__device__ __forceinline__ int stage_xtile(uint8_t *lq, uint8_t *ls, const uint8_t *x,
+                                           const uint8_t *xs, int k, int tokens, RowIdx row_idx) {
   const int stride = xtile_stride(k), sstride = xtile_sstride(k);
+  const int T4 = (tokens + 3) & ~3, nrows = Split ? 2 * T4 : tokens;
   const int pieces = (stride - 16) >> 4;  // includes the trailing zero chunk
   const bool aligned = ((((uintptr_t)x) | (uintptr_t)k) & 15u) == 0;
-  for (int p = threadIdx.x; p < tokens * pieces; p += blockDim.x) {
-    int r = p / pieces, off = (p - r * pieces) << 4;
+  for (int p = threadIdx.x; p < nrows * pieces; p += blockDim.x) {
+    const int r = p / pieces, off = (p - r * pieces) << 4;
+    const bool big = !Split || r < T4;
+    const int t = big ? r : r - T4;
     uint4 v = make_uint4(0, 0, 0, 0);
-    const uint8_t *src = x + (size_t)row_idx(r) * k + off;
-    if (off < k) {
+    if (t < tokens && off < k) {
+      const uint8_t *src = x + (size_t)row_idx(t) * k + off;
       if (aligned) v = *reinterpret_cast<const uint4 *>(src);
       else {
         uint8_t b[16];
         for (int i = 0; i < 16; ++i) b[i] = src[i];
         v = *reinterpret_cast<const uint4 *>(b);
       }
+      if (Split) {
+        const uint32_t f = big ? 0u : 0xffffffffu;
+        v.x &= e4m3_big_mask(v.x) ^ f;
+        v.y &= e4m3_big_mask(v.y) ^ f;
+        v.z &= e4m3_big_mask(v.z) ^ f;
+        v.w &= e4m3_big_mask(v.w) ^ f;
+      }
     }
     *reinterpret_cast<uint4 *>(lq + r * stride + off) = v;
   }
   const int ng = k >> 5;
-  for (int p = threadIdx.x; p < tokens * sstride; p += blockDim.x) {
-    int r = p / sstride, g = p - r * sstride;
-    ls[r * sstride + g] = g < ng ? xs[(size_t)row_idx(r) * ng + g] : (uint8_t)127;
+  for (int p = threadIdx.x; p < nrows * sstride; p += blockDim.x) {
+    const int r = p / sstride, g = p - r * sstride;
+    const int t = (!Split || r < T4) ? r : r - T4;
+    ls[r * sstride + g] = g < ng && t < tokens ? xs[(size_t)row_idx(t) * ng + g] : (uint8_t)127;
   }
+  return nrows;
 }
 
 // Operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950):
@@ -148,6 +187,19 @@ __device__ __forceinline__ void stage_xtile(uint8_t *lq, uint8_t *ls, const uint
 // only the older batch. All weight loads are unconditional: lanes past the last
 // K32 group re-read a valid group and get scale 127 against zero activations,
 // and a partial last batch re-reads the last chunk without computing it.
+// One 128-k chunk of the scaled MFMA (A = 16 activation rows, lo/hi = this
+// lane's two 16-byte pieces of k 16q..16q+15 and 64+16q..64+16q+15, q = l>>4;
+// B = weights) accumulated into acc. Measured on gfx950: the result equals four
+// single-K32-group MFMAs into fresh accumulators added to acc in k order in
+// fp32 (the reference's one block-scaled MMA per k32 plus serial fp32 add,
+// components/moe/src/mxfp4.cu:113-132), bit for bit, so one instruction does it.
+template <bool Split>
+__device__ __forceinline__ v4f mfma_chunk(const uint4 &lo, const uint4 &hi, const v8i &bv, v4f acc, int sa, int sw) {
+  static_assert(!Split, "magnitude split is done by the callers (split rows or a second accumulator)");
+  const v8i a = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bv, acc, 0, 4, 0, sa, 0, sw);
+}
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef const u32x4 __attribute__((address_space(1))) *global_u4;
@@ -200,11 +252,10 @@ struct Gemv16 {
       const int cx = c < nch ? c : nch;  // nch is the zero chunk
       const uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * cx);
       const uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * cx + 64);
-      const v8i a = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
       const v8i bv = v8i{(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w, 0, 0, 0, 0};
       int g = 4 * c + kb;
       g = g < ng ? g : ng - 1;
-      acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bv, acc, 0, 4, 0, (int)sa[4 * cx], 0, (int)lsw[g]);
+      acc = mfma_chunk<false>(lo, hi, bv, acc, (int)sa[4 * cx], (int)lsw[g]);
     };
     auto compute = [&](const uint4 *buf, int b) {
 #pragma unroll

@@ -45,6 +45,15 @@ class MoeLayerArgs(ctypes.Structure):
                 ("stage_events", ctypes.c_void_p)]
 
 
+class MoePrefillArgs(ctypes.Structure):
+    _fields_ = [("x_bf16", ctypes.c_void_p), ("ids", ctypes.c_void_p), ("weights", ctypes.c_void_p),
+                ("table", ctypes.c_void_p), ("expert_base", ctypes.c_int32), ("shared_index", ctypes.c_int32),
+                ("tokens", ctypes.c_int32), ("hidden", ctypes.c_int32), ("inter", ctypes.c_int32),
+                ("n_experts", ctypes.c_int32), ("topk", ctypes.c_int32), ("swiglu_limit", ctypes.c_float),
+                ("y_bf16", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+                ("stage_events", ctypes.c_void_p)]
+
+
 class ExpertLayout(ctypes.Structure):
     _fields_ = [("offset", ctypes.c_uint64 * 6), ("bytes", ctypes.c_uint64)]
 
@@ -87,6 +96,7 @@ def lib():
             raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
         _lib = ctypes.CDLL(LIB_PATH)
         _lib.ds41_moe_layer_workspace_bytes.restype = ctypes.c_size_t
+        _lib.ds41_moe_prefill_workspace_bytes.restype = ctypes.c_size_t
         _lib.ds41_gfx950_version.restype = ctypes.c_char_p
         _lib.ds41_spark_accept_workspace_bytes.restype = ctypes.c_size_t
         _lib.ds41_spark_verify_logits_gpu_v2.argtypes = [
@@ -417,3 +427,44 @@ class VerifyStack:
             self.close()
         except Exception:
             pass
+
+
+# ---- chunked verify / prefill ---------------------------------------------------------
+def prefill_raw(w, ws, xq, xs, m, n, k, out=None, stream=None):
+    import torch
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=w.device)
+    check(lib().ds41_mxfp4_prefill_raw(_p(w), _p(ws), _p(xq), _p(xs), _p(out), m, n, k, _stream(stream)),
+          "ds41_mxfp4_prefill_raw")
+    return out
+
+
+def grouped_prefill(table, jobs, count, projection, n, k, max_tokens, stream=None):
+    check(lib().ds41_grouped_mxfp4_prefill(_p(table), _p(jobs), count, projection, n, k, max_tokens,
+                                           _stream(stream)), "ds41_grouped_mxfp4_prefill")
+
+
+def prefill_workspace_bytes(T, H, I, E, K):
+    return lib().ds41_moe_prefill_workspace_bytes(T, H, I, E, K)
+
+
+def make_prefill_args(x, ids, weights, table, expert_base, shared_index, T, H, I, E, K, y, workspace,
+                      swiglu_limit=10.0):
+    a = MoePrefillArgs()
+    a.x_bf16, a.ids, a.weights, a.table = x.data_ptr(), ids.data_ptr(), weights.data_ptr(), table.data_ptr()
+    a.expert_base, a.shared_index = expert_base, shared_index
+    a.tokens, a.hidden, a.inter, a.n_experts, a.topk = T, H, I, E, K
+    a.swiglu_limit = swiglu_limit
+    a.y_bf16, a.workspace, a.workspace_bytes = y.data_ptr(), workspace.data_ptr(), workspace.numel()
+    return a
+
+
+def moe_prefill(args, stream=None):
+    check(lib().ds41_moe_prefill_layer(ctypes.byref(args), _stream(stream)), "ds41_moe_prefill_layer")
+
+
+def prefill_tiles(workspace, T, H, I, E, K):
+    v = ctypes.c_int32(0)
+    check(lib().ds41_moe_prefill_tiles(ctypes.c_void_p(workspace.data_ptr()), T, H, I, E, K, ctypes.byref(v)),
+          "ds41_moe_prefill_tiles")
+    return v.value

@@ -154,6 +154,50 @@ int ds41_moe_verify_layer(const ds41_moe_layer_args *args, void *stream);
 int ds41_moe_layer_plan(const void *workspace, int tokens, int hidden, int inter, int n_experts,
                         int topk, int32_t *unique_ids, int max_ids);
 
+/* ---- chunked verify / prefill (T >= 256 rows) on the scaled MFMA ------------- */
+/* grouped_mxfp4_prefill (components/moe/src/mxfp4.cu:382-385, prefill.cuh:7-96):
+ * jobs of 1..max_tokens (<= 256) rows; grid over 64-channel x 64-row tiles.
+ * k % 32 == 0 (the reference requires k % 256 == 0). Job x / x_scale rows must
+ * be 16-byte aligned (x: k bytes per row). A job whose token count is outside
+ * 1..max_tokens is skipped and sets status bit 2. */
+int ds41_grouped_mxfp4_prefill(const ds41_device_expert *table, const ds41_gemm_job *jobs,
+                               int count, int projection, int n, int k, int max_tokens,
+                               void *stream);
+/* ds41_mxfp4_prefill_raw (mxfp4.cu:436-442): one job, m <= 256 rows. */
+int ds41_mxfp4_prefill_raw(const uint8_t *weight, const uint8_t *weight_scale,
+                           const uint8_t *activation, const uint8_t *activation_scale,
+                           void *output_bf16, int m, int n, int k, void *stream);
+
+/* One prefill MoE layer over T = tokens rows (engine/src/prefill/native.inc:240-276
+ * with engine/include/ds41/prefill/plan.hpp:39-54): MXFP8 quantisation of x, a
+ * device route plan (stable expert-major permutation of the T*topk slots,
+ * per-expert offsets, <= 64-row tiles), fused gate/up GEMM + SwiGLU(limit)*w +
+ * MXFP8, down GEMM, and the ordered reduce (ascending expert id, shared last).
+ * ids / weights: device [tokens][topk] routing (the caller's top-k). Invalid or
+ * duplicate ids: every output row is NaN and status bit 4 is set.
+ * tokens * topk <= 4096, topk <= 8, n_experts <= 1024, hidden % 64 == 0,
+ * inter % 32 == 0. */
+typedef struct ds41_moe_prefill_args {
+  const void *x_bf16;             /* [tokens][hidden] */
+  const int32_t *ids;             /* [tokens][topk] */
+  const float *weights;           /* [tokens][topk] */
+  const ds41_device_expert *table;
+  int32_t expert_base, shared_index;
+  int32_t tokens, hidden, inter, n_experts, topk;
+  float swiglu_limit;
+  void *y_bf16;                   /* [tokens][hidden] */
+  void *workspace;                /* ds41_moe_prefill_workspace_bytes() device bytes */
+  size_t workspace_bytes;
+  void *const *stage_events;      /* optional: 6 hipEvent_t around the 5 kernels */
+} ds41_moe_prefill_args;
+size_t ds41_moe_prefill_workspace_bytes(int tokens, int hidden, int inter, int n_experts,
+                                        int topk);
+int ds41_moe_prefill_layer(const ds41_moe_prefill_args *args, void *stream);
+/* Number of GEMM tiles the last prefill plan produced (synchronous read; 0 after
+ * invalid routes). */
+int ds41_moe_prefill_tiles(const void *workspace, int tokens, int hidden, int inter,
+                           int n_experts, int topk, int32_t *tiles);
+
 /* ---- verify step through a stack of MoE layers with a host expert tier ------ */
 /* Canonical expert slab (the reference's 18.8 MB offload slot, store.hpp:32-37,
  * offload.cpp:443-457): gate W [inter][hidden/2] | gate scales [inter][hidden/32]

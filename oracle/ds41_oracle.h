@@ -63,7 +63,8 @@ int oracle_mxfp4_gemm(const uint8_t *w, const uint8_t *ws, const uint8_t *x, con
 
 /* SwiGLU (+route weight), components/moe/src/mxfp4.cu:323-332 swiglu_kernel:
  * g = min(g, L); u = clamp(u, -L, L) (only when L > 0); h = fp32(fp32(g / fp32(1 + expf(-g))) * u);
- * h = fp32(w[row] * h) when w != NULL; out = bf16(h). glibc expf stands in for CUDA expf.
+ * h = fp32(w[row] * h) when w != NULL; out = bf16(h). expf is evaluated as (float)exp((double)x),
+ * the correctly rounded value for practical inputs, in place of CUDA expf (within 2 ulp of it).
  * Pinned by the formula (tests/test_oracle_moe.py swiglu test); bitwise parity with the
  * reference's CUDA expf rounding is unpinned (compared within tolerance only). */
 void oracle_swiglu(const uint16_t *g, const uint16_t *u, const float *w, uint16_t *out,
@@ -76,7 +77,8 @@ void oracle_swiglu(const uint16_t *g, const uint16_t *u, const float *w, uint16_
  * PARITY UNPINNED against the reference's bits (no reference test or fixture fixes the
  * logits); pinned only to the exact dot product (fp64 check in tests/test_oracle_moe.py). */
 void oracle_router_logits(const uint16_t *x, const float *wg, int m, int e, int h, float *logits);
-/* components/dense/src/ops.cu:73 router: u = sqrt(z > 20 ? z : log1p(exp(z))), b = u + bias.
+/* components/dense/src/ops.cu:73 router: u = sqrt(z > 20 ? z : log1p(exp(z))), b = u + bias
+ * (exp and log1p as the fp32 rounding of the fp64 functions).
  * mode 1 replaces the score by the logistic sigmoid 1/(1+exp(-z)) (a labelled synthetic mode). */
 void oracle_router_scores(const float *logits, const float *bias, int m, int n, int mode,
                           float *u, float *b);

@@ -190,6 +190,11 @@ int oracle_mxfp4_gemm(const uint8_t *w, const uint8_t *ws, const uint8_t *x, con
   return gemm_impl(w, ws, x, xs, m, n, k, acc_out, out_bf16, gemm_threads);
 }
 
+/* exp / log1p as the fp32 rounding of the fp64 function (the correctly rounded fp32 value for all
+ * practical inputs); the GPU kernels evaluate the same expression. */
+static float exp_f32(float x) { return (float)exp((double)x); }
+static float log1p_f32(float x) { return (float)log1p((double)x); }
+
 void oracle_swiglu(const uint16_t *g, const uint16_t *u, const float *w, uint16_t *out, int rows,
                    int cols, float limit) {
   for (int r = 0; r < rows; ++r)
@@ -197,7 +202,7 @@ void oracle_swiglu(const uint16_t *g, const uint16_t *u, const float *w, uint16_
       size_t i = (size_t)r * cols + c;
       float gv = oracle_bf16_to_f32(g[i]), uv = oracle_bf16_to_f32(u[i]);
       if (limit > 0) { gv = fminf(gv, limit); uv = fminf(limit, fmaxf(-limit, uv)); }
-      float den = 1.0f + expf(-gv);
+      float den = 1.0f + exp_f32(-gv);
       float h = (gv / den) * uv;
       if (w) h = w[r] * h;
       out[i] = oracle_f32_to_bf16(h);
@@ -218,8 +223,8 @@ void oracle_router_scores(const float *logits, const float *bias, int m, int n, 
                           float *b) {
   for (int i = 0; i < m * n; ++i) {
     float z = logits[i], v;
-    if (mode == 1) v = 1.0f / (1.0f + expf(-z));
-    else v = sqrtf(z > 20.0f ? z : log1pf(expf(z)));
+    if (mode == 1) v = 1.0f / (1.0f + exp_f32(-z));
+    else v = sqrtf(z > 20.0f ? z : log1p_f32(exp_f32(z)));
     u[i] = v;
     b[i] = v + bias[i % n];
   }
