@@ -138,6 +138,82 @@ def bench_accept(gpu, steps, cpu_seconds, no_cpu):
             "bytes_per_step": 7 * V * 4, "cpu_baseline": cpu}
 
 
+PEAK_FP4_TFLOPS = 10100.0
+
+
+def bench_prefill(gpu, table, E, steps, warmup, seed=3):
+    """one MoE layer chunked verify/prefill, T=512 rows bf16 N(0,1), each token routed to K=6
+    distinct experts drawn from Zipf(1.1) over ranks (rank r -> expert perm[r-1], seeded permutation), route
+    weights random positive normalised to 1.5 per token (labelled: the configs[3] text leaves them open),
+    same 384+1 experts as configs[1]. A step is one prefill layer: MXFP8 quantisation, device route plan,
+    gate/up + SwiGLU + MXFP8, down, ordered reduce."""
+    import numpy as np
+    import torch
+    import ds41_gfx950 as G
+    T, H, I, K = 512, 4096, 2880, 6
+    rng = np.random.default_rng(seed)
+    p = np.arange(1, E + 1, dtype=np.float64) ** -1.1
+    p /= p.sum()
+    perm = rng.permutation(E)
+    ids_np = np.stack([perm[rng.choice(E, size=K, replace=False, p=p)] for _ in range(T)]).astype(np.int32)
+    w_np = (rng.random((T, K)) + 0.1).astype(np.float32)
+    w_np = (w_np / w_np.sum(axis=1, keepdims=True) * 1.5).astype(np.float32)
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    x = torch.randn((T, H), generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
+    ids, w = torch.from_numpy(ids_np).to(gpu), torch.from_numpy(w_np).to(gpu)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(G.prefill_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
+    args = G.make_prefill_args(x, ids, w, table, 0, E, T, H, I, E, K, y, ws)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        G.moe_prefill(args, stream)
+    torch.cuda.synchronize()
+    tiles = G.prefill_tiles(ws, T, H, I, E, K)
+    ev = G.Events(2)
+    ev.record(0, stream)
+    for _ in range(steps):
+        G.moe_prefill(args, stream)
+    ev.record(1, stream)
+    torch.cuda.synchronize()
+    us = ev.elapsed(0, 1) * 1e3 / steps
+    NS = 6
+    st = G.Events(NS * steps)
+    names = ["quant", "plan", "gate_up_act", "down", "reduce"]
+    tot = {n: 0.0 for n in names}
+    for i in range(steps):
+        args.stage_events = st.ptr(NS * i)
+        G.moe_prefill(args, stream)
+    args.stage_events = None
+    torch.cuda.synchronize()
+    for i in range(steps):
+        for j, n in enumerate(names):
+            tot[n] += st.elapsed(NS * i + j, NS * i + j + 1) * 1e3 / steps
+    if G.take_status():
+        raise AssertionError("prefill bench: kernel status bits set")
+    U = int(np.unique(ids_np).size)
+    rows = T * K + T
+    weight_bytes = (U + 1) * EXPERT_BYTES
+    act_bytes = T * H * 2 * 2 + rows * (I + I // 32) * 2 + rows * H * 2 * 2  # x in, y out, activation/down rows
+    flops = 2.0 * rows * 3 * I * H
+    gu_bytes = (U + 1) * GATE_UP_BYTES
+    counts = np.bincount(ids_np.ravel(), minlength=E)
+    out = {"workload": "configs[3]: one MoE layer chunked verify/prefill, T=512, hidden 4096, 384 experts "
+                       "(I=2880, MXFP4) top-6 Zipf(1.1) + 1 shared; route weights random, normalised to 1.5",
+           "steps": steps, "us_per_layer": us, "tokens_per_s": T / (us * 1e-6),
+           "unique_experts": U, "max_rows_per_expert": int(counts.max()), "tiles": tiles,
+           "hbm_bytes": weight_bytes + act_bytes, "hbm_gbps": (weight_bytes + act_bytes) / (us * 1e-6) / 1e9,
+           "hbm_frac": (weight_bytes + act_bytes) / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+           "gflop": flops / 1e9, "tflops": flops / (us * 1e-6) / 1e12,
+           "mfma_frac_fp4_peak": flops / (us * 1e-6) / 1e12 / PEAK_FP4_TFLOPS,
+           "stage_us": tot,
+           "gate_up_gbps": gu_bytes / (tot["gate_up_act"] * 1e-6) / 1e9,
+           "down_gbps": (U + 1) * DOWN_BYTES / (tot["down"] * 1e-6) / 1e9}
+    log(f"prefill: {us:.1f} us/layer ({T / (us * 1e-6):.0f} tok/s), U={U}, tiles {tiles}, HBM "
+        f"{out['hbm_gbps']:.0f} GB/s, {out['tflops']:.0f} TFLOP/s; stages " +
+        ", ".join(f"{n} {tot[n]:.1f}" for n in names))
+    return out
+
+
 def zipf_route_ids(rng, perms, pool, T, K, s=1.1):
     """[pool][L][T][K] int32: per token K distinct Zipf(s) ranks over 1..E (sequential draws without
     replacement), rank r -> expert perms[l][r-1]."""
@@ -261,6 +337,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--accept-steps", type=int, default=10000)
     ap.add_argument("--stack-steps", type=int, default=1000)
+    ap.add_argument("--prefill-steps", type=int, default=50)
     ap.add_argument("--stack-warmup", type=int, default=20)
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (HBM counter calibration) and exit")
@@ -371,6 +448,8 @@ def main():
         log(f"accept: {accept['us_per_step']:.1f} us/step, mean accepted drafts {accept['mean_accepted_drafts']:.2f}, "
             f"cpu {accept['cpu_baseline']}")
 
+    prefill = bench_prefill(gpu, table, E, args.prefill_steps, 5) if args.prefill_steps > 0 else None
+
     del P, experts, table, layer_args, ws
     torch.cuda.empty_cache()
     stack = bench_stack(gpu, args.stack_steps, args.stack_warmup) if args.stack_steps > 0 else None
@@ -392,6 +471,7 @@ def main():
         "cpu_baseline": cpu,
         "accept": accept,
         "step40": stack,
+        "prefill": prefill,
     }
     if stack and accept:  # acceptance time as a fraction of the 40-layer step (target < 3 %)
         out["accept"]["frac_of_step40"] = {m: accept["us_per_step"] * 1e-3 / r["ms_per_step"]

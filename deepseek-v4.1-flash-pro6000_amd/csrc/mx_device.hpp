@@ -193,11 +193,19 @@ __device__ __forceinline__ int stage_xtile(uint8_t *lq, uint8_t *ls, const uint8
 // single-K32-group MFMAs into fresh accumulators added to acc in k order in
 // fp32 (the reference's one block-scaled MMA per k32 plus serial fp32 add,
 // components/moe/src/mxfp4.cu:113-132), bit for bit, so one instruction does it.
-template <bool Split>
 __device__ __forceinline__ v4f mfma_chunk(const uint4 &lo, const uint4 &hi, const v8i &bv, v4f acc, int sa, int sw) {
-  static_assert(!Split, "magnitude split is done by the callers (split rows or a second accumulator)");
   const v8i a = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bv, acc, 0, 4, 0, sa, 0, sw);
+}
+// The same chunk as two operands: its bytes with |v| >= 1 and its bytes with |v| < 1.
+__device__ __forceinline__ void split_chunk(const uint4 &lo, const uint4 &hi, v8i &big, v8i &small) {
+  const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t m = e4m3_big_mask(w[i]);
+    big[i] = (int)(w[i] & m);
+    small[i] = (int)(w[i] & ~m);
+  }
 }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -255,7 +263,7 @@ struct Gemv16 {
       const v8i bv = v8i{(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w, 0, 0, 0, 0};
       int g = 4 * c + kb;
       g = g < ng ? g : ng - 1;
-      acc = mfma_chunk<false>(lo, hi, bv, acc, (int)sa[4 * cx], (int)lsw[g]);
+      acc = mfma_chunk(lo, hi, bv, acc, (int)sa[4 * cx], (int)lsw[g]);
     };
     auto compute = [&](const uint4 *buf, int b) {
 #pragma unroll
