@@ -5,3 +5,4 @@
 #include "prefill.inc"
 #include "verify_stack.inc"
 #include "accept.inc"
+#include "spark_gpu.inc"

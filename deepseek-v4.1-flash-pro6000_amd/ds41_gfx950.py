@@ -99,6 +99,11 @@ def lib():
         _lib.ds41_moe_prefill_workspace_bytes.restype = ctypes.c_size_t
         _lib.ds41_gfx950_version.restype = ctypes.c_char_p
         _lib.ds41_spark_accept_workspace_bytes.restype = ctypes.c_size_t
+        _lib.ds41_spark_verify_gpu_v2.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                                  ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64,
+                                                  ctypes.c_void_p, ctypes.c_void_p]
+        _lib.ds41_spark_sample_gpu_v2.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64,
+                                                  ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
         _lib.ds41_spark_verify_logits_gpu_v2.argtypes = [
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_double,
             ctypes.c_double, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
@@ -320,6 +325,25 @@ def result_tuple(buf):
     emitted = int(raw[6])
     return (tuple(int(v) for v in raw[:max(emitted, 0)]), int(raw[7]), int(raw[8]), int(raw[9])) if emitted >= 0 \
         else ((), -1, -1, -1)
+
+
+def verify_gpu_v2(drafts_dev, q, p, greedy, seed, step, out, stream=None):
+    """ds41_spark_verify_gpu_v2 over fp32 measures p [k+1][V], q [k][V] (None when greedy)."""
+    k, V = p.shape[0] - 1, p.shape[1]
+    check(lib().ds41_spark_verify_gpu_v2(_p(drafts_dev if k else None), _p(q), _p(p), k, V, greedy, seed, step,
+                                         _p(out), _stream(stream)), "ds41_spark_verify_gpu_v2")
+
+
+def sample_gpu_v2(p, seed, step, slot, purpose, out, stream=None):
+    check(lib().ds41_spark_sample_gpu_v2(_p(p), p.shape[0], seed, step, slot, purpose, _p(out), _stream(stream)),
+          "ds41_spark_sample_gpu_v2")
+
+
+def result_raw(buf):
+    """All fields of a ds41_spark_result held in a device tensor, including an invalid step's."""
+    import numpy as np
+    raw = buf.cpu().numpy().view(np.int32)
+    return (tuple(int(v) for v in raw[:6]), int(raw[6]), int(raw[7]), int(raw[8]), int(raw[9]))
 
 
 def accept_fallbacks(workspace, drafts, vocab):

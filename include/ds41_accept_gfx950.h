@@ -39,6 +39,20 @@ int ds41_spark_verify_logits_gpu_v2(const float *target_logits, const float *dra
                                     double temperature, double top_p, uint64_t seed, uint64_t step,
                                     ds41_spark_result *out, void *workspace, size_t workspace_bytes,
                                     int flags, void *stream);
+/* The spark GPU sampler over fp32 measures (engine/third_party/spark/src/sampling.cu:25-49,
+ * declared in spark.h:133-134): p [drafts+1][vocab] and q [drafts][vocab] (q may be NULL when
+ * greedy) are unnormalised non-negative fp32 measures; each row is normalised by its fp64
+ * mass, with the reference kernel's summation orders, so decisions and tokens equal its.
+ * Writes a device ds41_spark_result; an invalid row or draft id gives emitted == -1.
+ * One workgroup; no workspace. Returns the launch error (hipErrorInvalidValue for bad
+ * arguments, as the reference). */
+int ds41_spark_verify_gpu_v2(const int32_t *drafts_dev, const float *q, const float *p,
+                             int drafts, int vocab, int greedy, uint64_t seed, uint64_t step,
+                             ds41_spark_result *out, void *stream);
+/* sample_kernel (sampling.cu:23,48): one token of measure p with the v2 uniform of
+ * (seed, step, slot, purpose); -1 for an invalid row. out: device int32. */
+int ds41_spark_sample_gpu_v2(const float *p, int vocab, uint64_t seed, uint64_t step, uint32_t slot,
+                             uint32_t purpose, int32_t *out, void *stream);
 /* Number of accept steps that took the sequential path since the workspace was
  * zeroed (synchronous read). */
 int ds41_spark_accept_fallbacks(const void *workspace, int drafts, int vocab, uint32_t *count);

@@ -165,6 +165,19 @@ int oracle_accept_logits(const float *target_logits, const float *draft_logits,
                          const int32_t *drafts, int count, int n, double temperature,
                          double top_p, uint64_t seed, uint64_t step, oracle_spark_result *out,
                          double *p_out, double *q_out);
+/* The reference's GPU sampler over fp32 measures, normalised in fp64
+ * (engine/third_party/spark/src/sampling.cu:6-39,48-49 verify_kernel / sample_kernel with v2
+ * uniforms): the kernel's fp64 summation orders (256 strided sums + halving tree for a row's
+ * mass; 256 contiguous chunk sums + serial prefix + in-chunk scan for a draw). Pinned against the
+ * compiled reference host sampler where every sum is exact (integer measures over a power-of-two
+ * mass), by closed forms and by the distribution test of tests/test_oracle_sampler.py; the
+ * summation order itself, where sums round, is restated from the kernel and otherwise unpinned.
+ * Invalid rows or ids give emitted = -1 (the kernel's convention). Returns 0, or -1 for bad
+ * arguments. */
+int oracle_spark_verify_gpu_v2(const int32_t *d, const float *q, const float *p, int count, int n,
+                               int greedy, uint64_t seed, uint64_t step, oracle_spark_result *out);
+int oracle_spark_sample_gpu_v2(const float *p, int n, uint64_t seed, uint64_t step, uint32_t slot,
+                               uint32_t purpose, int32_t *out);
 const char *oracle_error(void);
 
 #ifdef __cplusplus

@@ -52,6 +52,10 @@ def lib():
         L.oracle_accept_logits.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_double,
                                            ctypes.c_uint64, ctypes.c_uint64, P, P, P]
         L.oracle_swiglu.argtypes = [P, P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        L.oracle_spark_verify_gpu_v2.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64,
+                                                 ctypes.c_uint64, P]
+        L.oracle_spark_sample_gpu_v2.argtypes = [P, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32,
+                                                 ctypes.c_uint32, P]
         L.oracle_route_weights.argtypes = [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, P]
         _lib = L
     return _lib
@@ -88,6 +92,10 @@ class SparkResult(ctypes.Structure):
 
     def as_tuple(self):
         return (tuple(self.tokens[:self.emitted]), self.accepted_drafts, self.accepted_input_rows, self.rejected)
+
+    def raw(self):
+        """Every field, including those of an invalid step (emitted == -1)."""
+        return (tuple(self.tokens), self.emitted, self.accepted_drafts, self.accepted_input_rows, self.rejected)
 
 
 class Expert(ctypes.Structure):
@@ -307,6 +315,25 @@ def accept_logits(target, draft, drafts, temperature, top_p, seed, step):
                                   ctypes.byref(r), ctypes.c_void_p(0), ctypes.c_void_p(0)):
         raise ValueError(lib().oracle_error().decode())
     return r
+
+
+def verify_gpu_v2(d, q, p, count, n, greedy, seed, step):
+    """The reference GPU sampler's arithmetic over fp32 measures (sampling.cu:6-39)."""
+    r = SparkResult()
+    d = np.ascontiguousarray(d, np.int32) if d is not None else None
+    q = np.ascontiguousarray(q, np.float32) if q is not None else None
+    if lib().oracle_spark_verify_gpu_v2(_ptr(d), _ptr(q), _ptr(np.ascontiguousarray(p, np.float32)), count, n,
+                                        greedy, seed, step, ctypes.byref(r)):
+        raise ValueError(lib().oracle_error().decode())
+    return r
+
+
+def sample_gpu_v2(p, seed, step, slot, purpose):
+    out = ctypes.c_int32(-2)
+    p = np.ascontiguousarray(p, np.float32)
+    if lib().oracle_spark_sample_gpu_v2(_ptr(p), p.shape[0], seed, step, slot, purpose, ctypes.byref(out)):
+        raise ValueError(lib().oracle_error().decode())
+    return out.value
 
 
 def sample_v2(p, seed, step, slot, purpose):

@@ -201,3 +201,132 @@ done:
   if (q && q != q_out) free(q);
   return rc;
 }
+
+/* ---- the reference's GPU sampler over fp32 measures -------------------------------------------
+ * engine/third_party/spark/src/sampling.cu, restated for one block of 256 threads executed in
+ * order. The fp64 summation orders are those of the kernel: mass = 256 strided per-thread sums
+ * then a halving tree (sampling.cu:6-7); draw = 256 contiguous chunk sums, a serial exclusive
+ * prefix over the chunks, and an in-chunk scan (sampling.cu:12-22). */
+#define GPU_THREADS 256
+
+/* sampling.cu:7 mass: non-finite or negative entries make the sum NaN. */
+static double gpu_mass(const float *p, int n) {
+  double sh[GPU_THREADS];
+  for (int t = 0; t < GPU_THREADS; ++t) {
+    double z = 0;
+    for (int i = t; i < n; i += GPU_THREADS) {
+      double x = p[i];
+      if (!isfinite(x) || x < 0) x = NAN;
+      z += x;
+    }
+    sh[t] = z;
+  }
+  for (int d = GPU_THREADS / 2; d; d >>= 1)
+    for (int t = 0; t < d; ++t) sh[t] += sh[t + d];
+  return sh[0];
+}
+
+/* sampling.cu:8 argmax of a row of finite values: the first maximum. */
+static int gpu_argmax(const float *p, int n) {
+  int b = 0;
+  for (int i = 1; i < n; ++i)
+    if (p[i] > p[b]) b = i;
+  return b;
+}
+
+static double gpu_value(const float *p, const float *q, int i, double pz, double qz) {
+  if (!q) return (double)p[i] / pz;
+  const double v = (double)p[i] / pz - (double)q[i] / qz;
+  return v > 0. ? v : 0.;  /* fmax(0., v); v is never NaN for valid rows */
+}
+
+/* sampling.cu:12-22 draw: -1 when no index is selected. */
+static int gpu_draw(const float *p, const float *q, int n, double pz, double qz, double u) {
+  const int chunk = (n + GPU_THREADS - 1) / GPU_THREADS;
+  double pre[GPU_THREADS + 1], sh[GPU_THREADS];
+  for (int t = 0; t < GPU_THREADS; ++t) {
+    const int begin = t * chunk, end = begin + chunk < n ? begin + chunk : n;
+    double z = 0;
+    for (int i = begin; i < end; ++i) z += gpu_value(p, q, i, pz, qz);
+    sh[t] = z;
+  }
+  double sum = 0;
+  for (int j = 0; j < GPU_THREADS; ++j) {
+    pre[j] = sum;
+    sum += sh[j];
+  }
+  pre[GPU_THREADS] = sum;
+  const double total = pre[GPU_THREADS], target = u * total;
+  int answer = n;
+  for (int t = 0; t < GPU_THREADS; ++t) {
+    if (!(total > 0 && target >= pre[t] && (t == GPU_THREADS - 1 || target < pre[t + 1]))) continue;
+    const int begin = t * chunk, end = begin + chunk < n ? begin + chunk : n;
+    double c = pre[t];
+    int last = -1;
+    for (int i = begin; i < end; ++i) {
+      const double v = gpu_value(p, q, i, pz, qz);
+      if (v > 0) last = i;
+      c += v;
+      if (target < c) {
+        if (i < answer) answer = i;
+        break;
+      }
+    }
+    if (answer == n && last >= 0) answer = last;
+  }
+  return answer == n ? -1 : answer;
+}
+
+/* sampling.cu:25-39 verify_kernel with v2 uniforms (ds41_spark_verify_gpu_v2, sampling.cu:49).
+ * Invalid rows or draft ids end the step with emitted = -1 and the fields gathered so far. */
+int oracle_spark_verify_gpu_v2(const int32_t *d, const float *q, const float *p, int count, int n, int greedy,
+                               uint64_t seed, uint64_t step, oracle_spark_result *out) {
+  if (!out || !p || count < 0 || count > 5 || n < 1 || (count && (!d || (!q && !greedy))))
+    return fail("verify_gpu_v2 arguments");
+  oracle_spark_result r;
+  memset(&r, 0, sizeof r);
+  for (int k = 0; k <= count; ++k) {
+    const float *pk = p + (size_t)k * n;
+    const double pz = gpu_mass(pk, n);
+    if (!(pz > 0) || !isfinite(pz)) { r.emitted = -1; *out = r; return 0; }
+    if (k == count) {
+      r.tokens[r.emitted++] = greedy ? gpu_argmax(pk, n)
+                                     : gpu_draw(pk, NULL, n, pz, 1, oracle_uniform_v2(seed, step, (uint32_t)k,
+                                                                                     PURPOSE_TARGET, 0));
+      break;
+    }
+    const int token = d[k];
+    if (token < 0 || token >= n) { r.emitted = -1; *out = r; return 0; }
+    const float *qk = q ? q + (size_t)k * n : NULL;
+    const double qz = greedy ? 1 : gpu_mass(qk, n);
+    if (!greedy && (!(qz > 0) || !isfinite(qz) || !(qk[token] > 0))) { r.emitted = -1; *out = r; return 0; }
+    int accept;
+    if (greedy) accept = token == gpu_argmax(pk, n);
+    else {
+      const double ratio = ((double)pk[token] / pz) / ((double)qk[token] / qz);
+      accept = oracle_uniform_v2(seed, step, (uint32_t)k, PURPOSE_ACCEPT, 0) < (ratio < 1. ? ratio : 1.);
+    }
+    if (accept) {
+      r.tokens[r.emitted++] = token;
+      ++r.accepted_drafts;
+    } else {
+      r.tokens[r.emitted++] = greedy ? gpu_argmax(pk, n)
+                                     : gpu_draw(pk, qk, n, pz, qz,
+                                                oracle_uniform_v2(seed, step, (uint32_t)k, PURPOSE_RESIDUAL, 0));
+      r.rejected = 1;
+      break;
+    }
+  }
+  r.accepted_input_rows = r.accepted_drafts + 1;
+  *out = r;
+  return 0;
+}
+
+/* sampling.cu:23,48 sample_kernel / ds41_spark_sample_gpu_v2: -1 for an invalid row. */
+int oracle_spark_sample_gpu_v2(const float *p, int n, uint64_t seed, uint64_t step, uint32_t slot, uint32_t purpose,
+                               int32_t *out) {
+  if (!p || !out || n < 1 || purpose > 3 || slot > 5) return fail("sample_gpu_v2 arguments");
+  const double z = gpu_mass(p, n);
+  *out = (!(z > 0) || !isfinite(z)) ? -1 : gpu_draw(p, NULL, n, z, 1, oracle_uniform_v2(seed, step, slot, purpose, 0));
+  return 0;
+}
