@@ -65,10 +65,11 @@ def cpu_baseline(x_np, wg_np, bias_np, experts_gpu, H, I, E, seconds):
                       f"shared) of the C oracle, {per * 1e3:.1f} ms each"}
 
 
-def bench_accept(gpu, steps, cpu_seconds, no_cpu):
-    """acceptance alone, k=3 drafts + 1 bonus over V=129280, T=1.0, top-p 1.0, Philox-seeded,
-    `steps` consecutive steps over a pool of 16 resident logit sets (target N(0, 2.5^2), draft = target +
-    N(0, 0.5^2)); drafts sampled from q (slot k, purpose Draft) as the drafter does."""
+def bench_accept(gpu, steps, cpu_seconds, no_cpu, top_p=1.0):
+    """acceptance alone, k=3 drafts + 1 bonus over V=129280, T=1.0, top-p 1.0 (and the same
+    with top-p 0.95), Philox-seeded, `steps` consecutive steps over a pool of 16 resident logit sets
+    (target N(0, 2.5^2), draft = target + N(0, 0.5^2)); drafts sampled from q (slot k, purpose Draft) as
+    the drafter does."""
     import numpy as np
     import torch
     import ds41_gfx950 as G
@@ -79,7 +80,7 @@ def bench_accept(gpu, steps, cpu_seconds, no_cpu):
     for i in range(pool):
         t = (rng.standard_normal((k + 1, V)) * 2.5).astype(np.float32)
         d = (t[:k] + rng.standard_normal((k, V)) * 0.5).astype(np.float32)
-        q = [O.probabilities(d[j], 1.0, 1.0) for j in range(k)]
+        q = [O.probabilities(d[j], 1.0, top_p) for j in range(k)]
         ids.append([O.sample_v2(q[j], seed, i, j, 1) for j in range(k)])
         tgt.append(t)
         drf.append(d)
@@ -90,12 +91,12 @@ def bench_accept(gpu, steps, cpu_seconds, no_cpu):
     out = torch.zeros((steps, 16), dtype=torch.int32, device=gpu)
     stream = torch.cuda.current_stream()
     for s in range(50):
-        G.verify_logits(T_dev[s % pool], D_dev[s % pool], I_dev[s % pool], 1.0, 1.0, seed, s, out[s], ws)
+        G.verify_logits(T_dev[s % pool], D_dev[s % pool], I_dev[s % pool], 1.0, top_p, seed, s, out[s], ws)
     ev = G.Events(2)
     torch.cuda.synchronize()
     ev.record(0, stream)
     for s in range(steps):
-        G.verify_logits(T_dev[s % pool], D_dev[s % pool], I_dev[s % pool], 1.0, 1.0, seed, s, out[s], ws)
+        G.verify_logits(T_dev[s % pool], D_dev[s % pool], I_dev[s % pool], 1.0, top_p, seed, s, out[s], ws)
     ev.record(1, stream)
     torch.cuda.synchronize()
     us = ev.elapsed(0, 1) * 1e3 / steps
@@ -103,7 +104,7 @@ def bench_accept(gpu, steps, cpu_seconds, no_cpu):
     accepted = float(np.mean(res[:, 7]))
     # parity spot check of the timed results against the oracle (every 500th step)
     for s in range(0, steps, 500):
-        ref = O.accept_logits(tgt[s % pool], drf[s % pool], np.array(ids[s % pool], np.int32), 1.0, 1.0, seed, s)
+        ref = O.accept_logits(tgt[s % pool], drf[s % pool], np.array(ids[s % pool], np.int32), 1.0, top_p, seed, s)
         if G.result_tuple(out[s]) != ref.as_tuple():
             raise AssertionError(f"accept parity failed at step {s}")
     cpu = None
@@ -119,20 +120,20 @@ def bench_accept(gpu, steps, cpu_seconds, no_cpu):
                 p = np.empty((k + 1, V), np.float64)
                 q = np.empty((k, V), np.float64)
                 for j in range(k):
-                    R.ds41_spark_probabilities(drf[s % pool][j].ctypes.data, q[j].ctypes.data, V, 1.0, 1.0)
+                    R.ds41_spark_probabilities(drf[s % pool][j].ctypes.data, q[j].ctypes.data, V, 1.0, top_p)
                 for j in range(k + 1):
-                    R.ds41_spark_probabilities(x[j].ctypes.data, p[j].ctypes.data, V, 1.0, 1.0)
+                    R.ds41_spark_probabilities(x[j].ctypes.data, p[j].ctypes.data, V, 1.0, top_p)
                 d = np.array(ids[s % pool], np.int32)
                 r = O.SparkResult()
                 R.ds41_spark_verify_v2(d.ctypes.data, q.ctypes.data, p.ctypes.data, k, V, 0, seed, s,
                                        ctypes.byref(r))
             else:
-                O.accept_logits(x, drf[s % pool], np.array(ids[s % pool], np.int32), 1.0, 1.0, seed, s)
+                O.accept_logits(x, drf[s % pool], np.array(ids[s % pool], np.int32), 1.0, top_p, seed, s)
             n += 1
         per = (time.perf_counter() - t0) / n
         cpu = {"value": per * 1e6, "unit": "us/step", "cores": 1, "kind": kind,
                "sample": f"{n} accept steps (7 fp64 probability rows of V={V} + verify_v2), single thread"}
-    return {"workload": "configs[2]: accept k=3 + bonus, V=129280, T=1.0, top-p 1.0", "steps": steps,
+    return {"workload": f"configs[2]: accept k=3 + bonus, V=129280, T=1.0, top-p {top_p}", "steps": steps,
             "us_per_step": us, "mean_accepted_drafts": accepted,
             "sequential_path_steps": G.accept_fallbacks(ws, k, V),
             "bytes_per_step": 7 * V * 4, "cpu_baseline": cpu}
@@ -447,6 +448,11 @@ def main():
     if accept:
         log(f"accept: {accept['us_per_step']:.1f} us/step, mean accepted drafts {accept['mean_accepted_drafts']:.2f}, "
             f"cpu {accept['cpu_baseline']}")
+    accept_tp = bench_accept(gpu, max(args.accept_steps // 4, 1), min(args.cpu_seconds, 10.0), args.no_cpu, 0.95) \
+        if args.accept_steps > 0 else None
+    if accept_tp:
+        log(f"accept top-p 0.95: {accept_tp['us_per_step']:.1f} us/step, sequential-path steps "
+            f"{accept_tp['sequential_path_steps']}, cpu {accept_tp['cpu_baseline']}")
 
     prefill = bench_prefill(gpu, table, E, args.prefill_steps, 5) if args.prefill_steps > 0 else None
 
@@ -470,6 +476,7 @@ def main():
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, calibrated)"},
         "cpu_baseline": cpu,
         "accept": accept,
+        "accept_top_p": accept_tp,
         "step40": stack,
         "prefill": prefill,
     }
