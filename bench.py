@@ -102,6 +102,30 @@ def bench_accept(gpu, steps, cpu_seconds, no_cpu, top_p=1.0):
     us = ev.elapsed(0, 1) * 1e3 / steps
     res = out.cpu().numpy()
     accepted = float(np.mean(res[:, 7]))
+    # the same steps with the Python launch path taken out: `pool` consecutive steps captured in one HIP
+    # graph (kernels only, no memset nodes), replayed back to back; every replay's results are checked
+    gs = torch.cuda.Stream()
+    out_g = torch.zeros((pool, 16), dtype=torch.int32, device=gpu)
+    graph = torch.cuda.CUDAGraph()
+    gs.wait_stream(stream)
+    with torch.cuda.stream(gs):
+        G.verify_logits(T_dev[0], D_dev[0], I_dev[0], 1.0, top_p, seed, 0, out_g[0], ws)
+    gs.synchronize()
+    with torch.cuda.graph(graph, stream=gs):
+        for s in range(pool):
+            G.verify_logits(T_dev[s], D_dev[s], I_dev[s], 1.0, top_p, seed, s, out_g[s], ws)
+    reps = max(steps // pool, 1)
+    torch.cuda.synchronize()
+    ev.record(0, stream)
+    for _ in range(reps):
+        graph.replay()
+    ev.record(1, stream)
+    torch.cuda.synchronize()
+    us_graph = ev.elapsed(0, 1) * 1e3 / (reps * pool)
+    for s in range(pool):
+        ref = O.accept_logits(tgt[s], drf[s], np.array(ids[s], np.int32), 1.0, top_p, seed, s)
+        if G.result_tuple(out_g[s]) != ref.as_tuple():
+            raise AssertionError(f"accept graph-replay parity failed at step {s}")
     # parity spot check of the timed results against the oracle (every 500th step)
     for s in range(0, steps, 500):
         ref = O.accept_logits(tgt[s % pool], drf[s % pool], np.array(ids[s % pool], np.int32), 1.0, top_p, seed, s)
@@ -134,7 +158,7 @@ def bench_accept(gpu, steps, cpu_seconds, no_cpu, top_p=1.0):
         cpu = {"value": per * 1e6, "unit": "us/step", "cores": 1, "kind": kind,
                "sample": f"{n} accept steps (7 fp64 probability rows of V={V} + verify_v2), single thread"}
     return {"workload": f"configs[2]: accept k=3 + bonus, V=129280, T=1.0, top-p {top_p}", "steps": steps,
-            "us_per_step": us, "mean_accepted_drafts": accepted,
+            "us_per_step": us, "us_per_step_graph": us_graph, "mean_accepted_drafts": accepted,
             "sequential_path_steps": G.accept_fallbacks(ws, k, V),
             "bytes_per_step": 7 * V * 4, "cpu_baseline": cpu}
 
@@ -446,12 +470,14 @@ def main():
     accept = bench_accept(gpu, args.accept_steps, min(args.cpu_seconds, 10.0), args.no_cpu) \
         if args.accept_steps > 0 else None
     if accept:
-        log(f"accept: {accept['us_per_step']:.1f} us/step, mean accepted drafts {accept['mean_accepted_drafts']:.2f}, "
+        log(f"accept: {accept['us_per_step']:.1f} us/step ({accept['us_per_step_graph']:.1f} graph-replayed), "
+            f"mean accepted drafts {accept['mean_accepted_drafts']:.2f}, "
             f"cpu {accept['cpu_baseline']}")
     accept_tp = bench_accept(gpu, max(args.accept_steps // 4, 1), min(args.cpu_seconds, 10.0), args.no_cpu, 0.95) \
         if args.accept_steps > 0 else None
     if accept_tp:
-        log(f"accept top-p 0.95: {accept_tp['us_per_step']:.1f} us/step, sequential-path steps "
+        log(f"accept top-p 0.95: {accept_tp['us_per_step']:.1f} us/step ({accept_tp['us_per_step_graph']:.1f} "
+            f"graph-replayed), sequential-path steps "
             f"{accept_tp['sequential_path_steps']}, cpu {accept_tp['cpu_baseline']}")
 
     prefill = bench_prefill(gpu, table, E, args.prefill_steps, 5) if args.prefill_steps > 0 else None
