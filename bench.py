@@ -201,7 +201,7 @@ def bench_prefill(gpu, table, E, steps, warmup, seed=3):
     ev.record(1, stream)
     torch.cuda.synchronize()
     us = ev.elapsed(0, 1) * 1e3 / steps
-    NS = 6
+    NS = 10  # start/stop timestamps of each of the 5 kernels
     st = G.Events(NS * steps)
     names = ["quant", "plan", "gate_up_act", "down", "reduce"]
     tot = {n: 0.0 for n in names}
@@ -212,7 +212,7 @@ def bench_prefill(gpu, table, E, steps, warmup, seed=3):
     torch.cuda.synchronize()
     for i in range(steps):
         for j, n in enumerate(names):
-            tot[n] += st.elapsed(NS * i + j, NS * i + j + 1) * 1e3 / steps
+            tot[n] += st.elapsed(NS * i + 2 * j, NS * i + 2 * j + 1) * 1e3 / steps
     if G.take_status():
         raise AssertionError("prefill bench: kernel status bits set")
     U = int(np.unique(ids_np).size)
@@ -434,8 +434,8 @@ def main():
     total_ms = ev.elapsed(0, 1)
     ms_per_step = total_ms / args.steps
 
-    # per-kernel durations with stage events (a separate pass over the same steps)
-    NS = 6
+    # per-kernel execution times from start/stop timestamps (a separate pass over the same steps)
+    NS = 10
     stage = G.Events(NS * args.steps)
     for i in range(args.steps):
         a = layer_args[i % pool]
@@ -445,22 +445,46 @@ def main():
     torch.cuda.synchronize()
     names = ["router", "plan", "gate_up_act", "down", "reduce"]
     stage_ms = {n: 0.0 for n in names}
-    gate_bytes = down_bytes = 0
     for i in range(args.steps):
         for j, n in enumerate(names):
-            stage_ms[n] += stage.elapsed(NS * i + j, NS * i + j + 1)
-        u = uniq[i % pool]
-        gate_bytes += (u + 1) * GATE_UP_BYTES
-        down_bytes += (u + 1) * DOWN_BYTES
+            stage_ms[n] += stage.elapsed(NS * i + 2 * j, NS * i + 2 * j + 1)
     assert G.take_status() == 0
     avg = {n: stage_ms[n] / args.steps for n in names}
-    gate_gbps = gate_bytes / (stage_ms["gate_up_act"] * 1e-3) / 1e9
-    down_gbps = down_bytes / (stage_ms["down"] * 1e-3) / 1e9
+
+    # gate/up and down launched alone, back to back, over one prepared workspace per pool entry (each
+    # launch streams its own step's experts); events around the whole batch give the average launch
+    # duration of the kernel, the quantity the roofline divides by
+    wss = [torch.zeros_like(ws) for _ in range(pool)]
+    prep = [G.make_layer_args(x_pool[i], wg, bias, table, 0, E, T, H, I, E, K, y, wss[i]) for i in range(pool)]
+    for a in prep:
+        G.moe_layer(a, stream)
+    reps = max(args.steps // pool, 1)
+    launch_us = {}
+    for j, n in ((2, "gate_up_act"), (3, "down")):
+        for a in prep:
+            a.stage_mask = 1 << j
+        G.moe_layer(prep[-1], stream)
+        torch.cuda.synchronize()
+        ev.record(0, stream)
+        for _ in range(reps):
+            for a in prep:
+                G.moe_layer(a, stream)
+        ev.record(1, stream)
+        torch.cuda.synchronize()
+        launch_us[n] = ev.elapsed(0, 1) * 1e3 / (reps * pool)
+        for a in prep:
+            a.stage_mask = 0
+    assert G.take_status() == 0
+    mean_u = float(np.mean(uniq))
+    gate_gbps = (mean_u + 1) * GATE_UP_BYTES / (launch_us["gate_up_act"] * 1e-6) / 1e9
+    down_gbps = (mean_u + 1) * DOWN_BYTES / (launch_us["down"] * 1e-6) / 1e9
     layer_bytes = sum((uniq[i % pool] + 1) * EXPERT_BYTES + E * H * 4 for i in range(args.steps))
     layer_gbps = layer_bytes / (total_ms * 1e-3) / 1e9
-    log("stage avg us: " + ", ".join(f"{n} {avg[n] * 1e3:.1f}" for n in names))
+    log("stage avg us (start/stop timestamps, include dispatch): " +
+        ", ".join(f"{n} {avg[n] * 1e3:.1f}" for n in names))
+    log(f"launch avg us (back to back): gate_up_act {launch_us['gate_up_act']:.1f}, down {launch_us['down']:.1f}")
     log(f"gate_up_act {gate_gbps:.0f} GB/s, down {down_gbps:.0f} GB/s, layer {layer_gbps:.0f} GB/s "
-        f"({layer_gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s), mean unique experts {np.mean(uniq):.2f}")
+        f"({layer_gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s), mean unique experts {mean_u:.2f}")
 
     cpu = None
     if not args.no_cpu:
@@ -497,6 +521,7 @@ def main():
                    "mean_unique_experts": float(np.mean(uniq))},
         "hbm_gbps": layer_gbps, "hbm_frac": layer_gbps / PEAK_HBM_GBPS,
         "stage_us": {n: avg[n] * 1e3 for n in names},
+        "launch_us": launch_us,
         "roofline": {"bound": "hbm", "kernel": "layer_gate_up_act_kernel", "achieved": gate_gbps,
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": gate_gbps / PEAK_HBM_GBPS, "traffic": GATE_UP_TRAFFIC_BYTES,
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, calibrated)"},

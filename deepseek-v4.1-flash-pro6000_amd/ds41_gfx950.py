@@ -42,7 +42,7 @@ class MoeLayerArgs(ctypes.Structure):
                 ("y_bf16", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_size_t), ("ids_out", ctypes.c_void_p),
                 ("weights_out", ctypes.c_void_p), ("logits_out", ctypes.c_void_p),
-                ("stage_events", ctypes.c_void_p)]
+                ("stage_events", ctypes.c_void_p), ("stage_mask", ctypes.c_uint32)]
 
 
 class MoePrefillArgs(ctypes.Structure):

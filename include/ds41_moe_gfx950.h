@@ -141,9 +141,11 @@ typedef struct ds41_moe_layer_args {
   int32_t *ids_out;               /* optional [tokens][topk] (device) */
   float *weights_out;             /* optional [tokens][topk] (device) */
   float *logits_out;              /* optional [tokens][n_experts] (device) */
-  void *const *stage_events;      /* optional: 6 hipEvent_t recorded on `stream` before each of
-                                     the 5 kernels (router, plan, gate/up/act, down, reduce) and
-                                     after the last, for per-kernel timing */
+  void *const *stage_events;      /* optional: 10 hipEvent_t, the start and stop timestamps of
+                                     each of the 5 kernels (router, plan, gate/up/act, down,
+                                     reduce) in order (hipExtLaunchKernel) */
+  uint32_t stage_mask;            /* 0: every kernel. Otherwise bit i launches kernel i only (for
+                                     timing one kernel on a workspace a full call has prepared) */
 } ds41_moe_layer_args;
 size_t ds41_moe_layer_workspace_bytes(int tokens, int hidden, int inter, int n_experts,
                                       int topk);
@@ -188,7 +190,8 @@ typedef struct ds41_moe_prefill_args {
   void *y_bf16;                   /* [tokens][hidden] */
   void *workspace;                /* ds41_moe_prefill_workspace_bytes() device bytes */
   size_t workspace_bytes;
-  void *const *stage_events;      /* optional: 6 hipEvent_t around the 5 kernels */
+  void *const *stage_events;      /* optional: 10 hipEvent_t, start and stop of each of the 5
+                                     kernels (quant, plan, gate/up/act, down, reduce) */
 } ds41_moe_prefill_args;
 size_t ds41_moe_prefill_workspace_bytes(int tokens, int hidden, int inter, int n_experts,
                                         int topk);
