@@ -212,12 +212,21 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef const u32x4 __attribute__((address_space(1))) *global_u4;
 typedef const u32x2 __attribute__((address_space(1))) *global_u2;
+typedef u32x4 __attribute__((aligned(1))) u32x4_u;
+typedef const u32x4_u __attribute__((address_space(1))) *global_u4u;
 
-template <int U, bool Aligned16>
+// GScale: the weight scales come from global memory instead of an LDS row.
+// With each batch's weights a lane loads its channel's 32 scale bytes of that
+// batch (8 chunks x 4 groups; dword u holds chunk u's four groups) and takes
+// byte kb of each dword. Requires U == 8 and k % 1024 == 0 (whole batches).
+// Frees the workgroup's LDS of the weight scales.
+template <int U, bool Aligned16, bool GScale = false>
 struct Gemv16 {
   const uint8_t *w;  // weight row
+  const uint8_t *gs; // GScale: this lane's channel's scale row
   int kb, ng, nch, nb;
   uint4 A[U], B[U];
+  uint4 SA[2], SB[2];
 
   // 16 bytes of K32 group min(4c + kb, ng - 1) through a global-address-space
   // pointer (global_load, counted by vmcnt only, never by lgkmcnt). Plain (not
@@ -239,13 +248,22 @@ struct Gemv16 {
 #pragma unroll
     for (int u = 0; u < U; ++u) buf[u] = ld(b * U + u);
   }
-  __device__ __forceinline__ Gemv16(const uint8_t *wrow, int k) {
+  __device__ __forceinline__ void ld_scales(uint4 *S, int b) const {
+    // any alignment: gfx950 global loads take unaligned addresses (one dwordx4 either way)
+    const uint8_t *p = gs + 32 * b;
+    const u32x4 v0 = *(global_u4u)(p), v1 = *(global_u4u)(p + 16);
+    S[0] = make_uint4(v0.x, v0.y, v0.z, v0.w);
+    S[1] = make_uint4(v1.x, v1.y, v1.z, v1.w);
+  }
+  __device__ __forceinline__ Gemv16(const uint8_t *wrow, int k, const uint8_t *gscale_row = nullptr) {
     kb = (threadIdx.x & 63) >> 4;
     w = wrow;
+    gs = gscale_row;
     ng = k >> 5;
     nch = (ng + 3) >> 2;
     nb = (nch + U - 1) / U;
     load(A, 0);
+    if (GScale) ld_scales(SA, 0);
   }
   // xt: activation rows in LDS; lsw: this lane's weight-scale row in LDS (ng bytes).
   // Chunks past the end read the zero chunk of the activation rows (exact zero
@@ -256,32 +274,46 @@ struct Gemv16 {
     const uint8_t *xa = xt.q + ii * xt.stride + 16 * q;
     const uint8_t *sa = xt.s + ii * xt.sstride + q;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    auto mma = [&](const uint4 &wv, int c) {
+    auto mma = [&](const uint4 &wv, int c, int sw) {
       const int cx = c < nch ? c : nch;  // nch is the zero chunk
       const uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * cx);
       const uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * cx + 64);
       const v8i bv = v8i{(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w, 0, 0, 0, 0};
-      int g = 4 * c + kb;
-      g = g < ng ? g : ng - 1;
-      acc = mfma_chunk(lo, hi, bv, acc, (int)sa[4 * cx], (int)lsw[g]);
+      acc = mfma_chunk(lo, hi, bv, acc, (int)sa[4 * cx], sw);
     };
-    auto compute = [&](const uint4 *buf, int b) {
+    auto compute = [&](const uint4 *buf, const uint4 *S, int b) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) mma(buf[u], b * U + u);
+      for (int u = 0; u < U; ++u) {
+        const int c = b * U + u;
+        int sw;
+        if (GScale) {  // byte kb of dword u of the batch's scale window
+          const uint4 &w4 = S[u >> 2];
+          const uint32_t d = (u & 3) == 0 ? w4.x : (u & 3) == 1 ? w4.y : (u & 3) == 2 ? w4.z : w4.w;
+          sw = (int)((d >> (8 * kb)) & 0xffu);
+        } else {
+          int g = 4 * c + kb;
+          g = g < ng ? g : ng - 1;
+          sw = (int)lsw[g];
+        }
+        mma(buf[u], c, sw);
+      }
     };
     int b = 0;
     for (; b + 2 < nb; b += 2) {
       load(B, b + 1);
-      compute(A, b);
+      if (GScale) ld_scales(SB, b + 1);
+      compute(A, SA, b);
       load(A, b + 2);
-      compute(B, b + 1);
+      if (GScale) ld_scales(SA, b + 2);
+      compute(B, SB, b + 1);
     }
     if (b + 2 == nb) {
       load(B, b + 1);
-      compute(A, b);
-      compute(B, b + 1);
+      if (GScale) ld_scales(SB, b + 1);
+      compute(A, SA, b);
+      compute(B, SB, b + 1);
     } else {
-      compute(A, b);
+      compute(A, SA, b);
     }
     return acc;
   }
