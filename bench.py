@@ -201,18 +201,24 @@ def bench_prefill(gpu, table, E, steps, warmup, seed=3):
     ev.record(1, stream)
     torch.cuda.synchronize()
     us = ev.elapsed(0, 1) * 1e3 / steps
-    NS = 10  # start/stop timestamps of each of the 5 kernels
+    kernels = ["quant", "plan", "gate_up_gemv4", "gate_up_gemv8", "gate_up_tiles", "down_gemv4", "down_gemv8",
+               "down_tiles", "reduce"]
+    NS = 2 * len(kernels)  # start/stop timestamps of each kernel
     st = G.Events(NS * steps)
-    names = ["quant", "plan", "gate_up_act", "down", "reduce"]
-    tot = {n: 0.0 for n in names}
+    ktot = {n: 0.0 for n in kernels}
     for i in range(steps):
         args.stage_events = st.ptr(NS * i)
         G.moe_prefill(args, stream)
     args.stage_events = None
     torch.cuda.synchronize()
     for i in range(steps):
-        for j, n in enumerate(names):
-            tot[n] += st.elapsed(NS * i + 2 * j, NS * i + 2 * j + 1) * 1e3 / steps
+        for j, n in enumerate(kernels):
+            ktot[n] += st.elapsed(NS * i + 2 * j, NS * i + 2 * j + 1) * 1e3 / steps
+    names = ["quant", "plan", "gate_up_act", "down", "reduce"]
+    tot = {"quant": ktot["quant"], "plan": ktot["plan"],
+           "gate_up_act": ktot["gate_up_gemv4"] + ktot["gate_up_gemv8"] + ktot["gate_up_tiles"],
+           "down": ktot["down_gemv4"] + ktot["down_gemv8"] + ktot["down_tiles"], "reduce": ktot["reduce"]}
+    plan = G.prefill_plan_counts(ws, T, H, I, E, K)
     if G.take_status():
         raise AssertionError("prefill bench: kernel status bits set")
     U = int(np.unique(ids_np).size)
@@ -230,12 +236,13 @@ def bench_prefill(gpu, table, E, steps, warmup, seed=3):
            "hbm_frac": (weight_bytes + act_bytes) / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
            "gflop": flops / 1e9, "tflops": flops / (us * 1e-6) / 1e12,
            "mfma_frac_fp4_peak": flops / (us * 1e-6) / 1e12 / PEAK_FP4_TFLOPS,
-           "stage_us": tot,
+           "stage_us": tot, "kernel_us": ktot,
+           "plan": {"tiles": plan[0], "gemv_jobs_le4_rows": plan[1], "gemv_jobs_5to8_rows": plan[2]},
            "gate_up_gbps": gu_bytes / (tot["gate_up_act"] * 1e-6) / 1e9,
            "down_gbps": (U + 1) * DOWN_BYTES / (tot["down"] * 1e-6) / 1e9}
-    log(f"prefill: {us:.1f} us/layer ({T / (us * 1e-6):.0f} tok/s), U={U}, tiles {tiles}, HBM "
-        f"{out['hbm_gbps']:.0f} GB/s, {out['tflops']:.0f} TFLOP/s; stages " +
-        ", ".join(f"{n} {tot[n]:.1f}" for n in names))
+    log(f"prefill: {us:.1f} us/layer ({T / (us * 1e-6):.0f} tok/s), U={U}, plan (tiles, gemv<=4, gemv5-8) {plan}, "
+        f"HBM {out['hbm_gbps']:.0f} GB/s, {out['tflops']:.0f} TFLOP/s; kernels " +
+        ", ".join(f"{n} {ktot[n]:.1f}" for n in kernels))
     return out
 
 

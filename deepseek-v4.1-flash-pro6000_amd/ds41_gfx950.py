@@ -487,6 +487,14 @@ def moe_prefill(args, stream=None):
     check(lib().ds41_moe_prefill_layer(ctypes.byref(args), _stream(stream)), "ds41_moe_prefill_layer")
 
 
+def prefill_plan_counts(workspace, T, H, I, E, K):
+    """(tiles, GEMV jobs of experts with <= 4 rows, GEMV jobs of experts with 5..8 rows)."""
+    v = (ctypes.c_int32 * 3)()
+    check(lib().ds41_moe_prefill_plan_counts(ctypes.c_void_p(workspace.data_ptr()), T, H, I, E, K, v),
+          "ds41_moe_prefill_plan_counts")
+    return tuple(v)
+
+
 def prefill_tiles(workspace, T, H, I, E, K):
     v = ctypes.c_int32(0)
     check(lib().ds41_moe_prefill_tiles(ctypes.c_void_p(workspace.data_ptr()), T, H, I, E, K, ctypes.byref(v)),

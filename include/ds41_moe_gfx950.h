@@ -173,8 +173,10 @@ int ds41_mxfp4_prefill_raw(const uint8_t *weight, const uint8_t *weight_scale,
 /* One prefill MoE layer over T = tokens rows (engine/src/prefill/native.inc:240-276
  * with engine/include/ds41/prefill/plan.hpp:39-54): MXFP8 quantisation of x, a
  * device route plan (stable expert-major permutation of the T*topk slots,
- * per-expert offsets, <= 64-row tiles), fused gate/up GEMM + SwiGLU(limit)*w +
- * MXFP8, down GEMM, and the ordered reduce (ascending expert id, shared last).
+ * per-expert offsets; experts with <= 8 rows become GEMV jobs of the decode
+ * layer's kernels, the others and the shared expert <= 64-row tiles), fused
+ * gate/up + SwiGLU(limit)*w + MXFP8, down, and the ordered reduce (ascending
+ * expert id, shared last).
  * ids / weights: device [tokens][topk] routing (the caller's top-k). Invalid or
  * duplicate ids: every output row is NaN and status bit 4 is set.
  * tokens * topk <= 4096, topk <= 8, n_experts <= 1024, hidden % 64 == 0,
@@ -190,16 +192,23 @@ typedef struct ds41_moe_prefill_args {
   void *y_bf16;                   /* [tokens][hidden] */
   void *workspace;                /* ds41_moe_prefill_workspace_bytes() device bytes */
   size_t workspace_bytes;
-  void *const *stage_events;      /* optional: 10 hipEvent_t, start and stop of each of the 5
-                                     kernels (quant, plan, gate/up/act, down, reduce) */
+  void *const *stage_events;      /* optional: 18 hipEvent_t, start and stop of each of the 9
+                                     kernels: quant, plan, gate/up/act GEMV (<= 4 rows), GEMV
+                                     (5..8 rows), tiles, down GEMV (<= 4), GEMV (5..8), tiles,
+                                     reduce */
 } ds41_moe_prefill_args;
 size_t ds41_moe_prefill_workspace_bytes(int tokens, int hidden, int inter, int n_experts,
                                         int topk);
 int ds41_moe_prefill_layer(const ds41_moe_prefill_args *args, void *stream);
-/* Number of GEMM tiles the last prefill plan produced (synchronous read; 0 after
- * invalid routes). */
+/* Number of 64-row GEMM tiles the last prefill plan produced (experts with more
+ * than 8 rows, and the shared expert; synchronous read; 0 after invalid routes). */
 int ds41_moe_prefill_tiles(const void *workspace, int tokens, int hidden, int inter,
                            int n_experts, int topk, int32_t *tiles);
+/* The last prefill plan's work split (synchronous read): counts[0] tiles,
+ * counts[1] GEMV jobs of experts with <= 4 rows, counts[2] of experts with
+ * 5..8 rows. No counterpart in the reference (its sweep batches experts on the host). */
+int ds41_moe_prefill_plan_counts(const void *workspace, int tokens, int hidden, int inter,
+                                 int n_experts, int topk, int32_t *counts);
 
 /* ---- verify step through a stack of MoE layers with a host expert tier ------ */
 /* Canonical expert slab (the reference's 18.8 MB offload slot, store.hpp:32-37,

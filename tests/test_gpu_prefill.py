@@ -146,7 +146,17 @@ def run_prefill(gpu, experts, x_np, ids, w, H, I, E, K, shared=True):
                             K, y, ws)
     G.moe_prefill(a)
     torch.cuda.synchronize()
-    return host(y), G.prefill_tiles(ws, T, H, I, E, K)
+    plan = G.prefill_plan_counts(ws, T, H, I, E, K)
+    assert plan[0] == G.prefill_tiles(ws, T, H, I, E, K)
+    return host(y), plan
+
+
+def want_plan(counts, T):
+    """The plan's split: 64-row tiles for experts with more than 8 rows and for the shared expert's T
+    rows; GEMV jobs for the experts with 1..4 and with 5..8 rows."""
+    big = counts[counts > 8]
+    return (int(np.sum((big + 63) // 64)) + (T + 63) // 64, int(np.sum((counts >= 1) & (counts <= 4))),
+            int(np.sum((counts >= 5) & (counts <= 8))))
 
 
 def check_tokens(experts, x_np, ids, w, got, H, I, E, tokens):
@@ -159,7 +169,8 @@ def check_tokens(experts, x_np, ids, w, got, H, I, E, tokens):
     return rel_l2(O.bf16_to_f32(got[tokens]), O.bf16_to_f32(ref)), np.mean(got[tokens] == ref)
 
 
-@pytest.mark.parametrize("T,E,skew", [(300, 32, "uniform"), (256, 32, "zipf"), (77, 64, "zipf"), (1, 8, "uniform")])
+@pytest.mark.parametrize("T,E,skew", [(300, 32, "uniform"), (256, 32, "zipf"), (77, 64, "zipf"), (1, 8, "uniform"),
+                                      (40, 32, "uniform")])
 def test_prefill_layer_vs_oracle(gpu, T, E, skew):
     import ds41_gfx950 as G
     H, I, K = 512, 256, 6
@@ -174,10 +185,10 @@ def test_prefill_layer_vs_oracle(gpu, T, E, skew):
     G.take_status()
     got, tiles = run_prefill(gpu, experts, x_np, ids, w, H, I, E, K)
     counts = np.bincount(ids.ravel(), minlength=E)
-    want_tiles = int(np.sum((counts + 63) // 64)) + (T + 63) // 64
     err, exact = check_tokens(experts, x_np, ids, w, got, H, I, E, np.arange(T))
-    say(f"  rows per expert max {counts.max()}, tiles {tiles}, rel-L2 {err:.3e}, bf16 exact {exact:.4f}")
-    assert tiles == want_tiles
+    say(f"  rows per expert max {counts.max()}, plan (tiles, gemv<=4, gemv5-8) {tiles}, rel-L2 {err:.3e}, "
+        f"bf16 exact {exact:.4f}")
+    assert tiles == want_plan(counts, T)
     assert err <= 1e-3
     assert G.take_status() == 0
 
@@ -193,7 +204,7 @@ def test_prefill_layer_invalid_routes_nan(gpu):
     w = np.full((T, K), 0.25, np.float32)
     G.take_status()
     got, tiles = run_prefill(gpu, experts, x_np, ids, w, H, I, E, K)
-    assert tiles == 0 and np.all(np.isnan(O.bf16_to_f32(got)))
+    assert tiles == (0, 0, 0) and np.all(np.isnan(O.bf16_to_f32(got)))
     assert G.take_status() & 4
 
 
@@ -224,7 +235,7 @@ def test_prefill_layer_config3_shape(gpu):
     say(f"  unique experts {np.count_nonzero(counts)}, max rows {counts.max()}, tiles {tiles}, rel-L2 {err:.3e}, "
         f"bf16 exact {np.mean(got == ref):.4f}, per-token rel-L2 median {np.median(per_token):.2e} max "
         f"{per_token.max():.2e}")
-    assert tiles == int(np.sum((counts + 63) // 64)) + (T + 63) // 64
+    assert tiles == want_plan(counts, T)
     assert err <= 1e-3
     assert G.take_status() == 0
 
