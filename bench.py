@@ -246,6 +246,79 @@ def bench_prefill(gpu, table, E, steps, warmup, seed=3):
     return out
 
 
+def bench_drafter(gpu, steps, warmup, seed=6):
+    """The MTP drafter's routed-expert service (ds41_target_experts_fn, routed_spark): B=5 drafter rows,
+    hidden 5120, 3 stages x 128 experts (I=2304, MXFP4, all HBM-resident, 7.2 GB), top-3 per row from the
+    drafter's router top-3 (ds41_spark_topk3_gpu) over random scores; route weights random positive. A call
+    is one stage: MXFP8 quantisation, plan from the caller's ids, gate/up + SwiGLU + MXFP8, down into slots."""
+    import numpy as np
+    import torch
+    import ds41_gfx950 as G
+    H, I, E, R = 5120, 2304, 3 * 128, 5
+    g = torch.Generator(device=gpu).manual_seed(seed)
+
+    def rnd(shape, lo, hi):
+        return torch.randint(lo, hi, shape, dtype=torch.uint8, device=gpu, generator=g)
+
+    P = dict(gate=rnd((E, I, H // 2), 0, 256), gate_scale=rnd((E, I, H // 32), 119, 124),
+             up=rnd((E, I, H // 2), 0, 256), up_scale=rnd((E, I, H // 32), 119, 124),
+             down=rnd((E, H, I // 2), 0, 256), down_scale=rnd((E, H, I // 32), 119, 124))
+    table, _ = G.device_table([{k: v[e] for k, v in P.items()} for e in range(E)], gpu)
+    pool = 64
+    scores = torch.rand((pool, R, 128), generator=g, device=gpu)
+    ids = torch.stack([G.spark_topk3(scores[i]) for i in range(pool)])
+    w = torch.rand((pool, R, 3), generator=g, device=gpu) + 0.1
+    x = torch.randn((pool, R, H), generator=g, device=gpu).to(torch.bfloat16)
+    out = torch.empty((R, 3, H), dtype=torch.bfloat16, device=gpu)
+    stream = torch.cuda.current_stream()
+    svc = G.TargetExperts(table, 0, H, I, stream=stream)
+    for i in range(warmup):
+        svc(i % 3, x[i % pool], ids[i % pool], w[i % pool], out)
+    torch.cuda.synchronize()
+    ev = G.Events(2)
+    ev.record(0, stream)
+    for i in range(steps):
+        svc(i % 3, x[i % pool], ids[i % pool], w[i % pool], out)
+    ev.record(1, stream)
+    torch.cuda.synchronize()
+    us = ev.elapsed(0, 1) * 1e3 / steps
+    ev.record(0, stream)
+    for i in range(steps):
+        G.spark_topk3(scores[i % pool], stream)
+    ev.record(1, stream)
+    torch.cuda.synchronize()
+    top3_us = ev.elapsed(0, 1) * 1e3 / steps
+    names = ["quant", "plan", "gate_up_act", "down"]
+    NS = 2 * len(names)
+    st = G.Events(NS)
+    svc_t = G.TargetExperts(table, 0, H, I, stream=stream, events=st.ptr(0))
+    ktot = {n: 0.0 for n in names}
+    for i in range(steps):  # the handle's one event set is read back after every call
+        svc_t(i % 3, x[i % pool], ids[i % pool], w[i % pool], out)
+        torch.cuda.synchronize()
+        for j, n in enumerate(names):
+            ktot[n] += st.elapsed(2 * j, 2 * j + 1) * 1e3 / steps
+    svc_t.close()
+    svc.close()
+    if G.take_status():
+        raise AssertionError("drafter bench: kernel status bits set")
+    ids_np = ids.cpu().numpy()
+    U = float(np.mean([np.unique(ids_np[i % pool]).size for i in range(steps)]))
+    ebytes = 3 * (I * H // 2) + 3 * (I * H // 32)
+    gu_bytes = 2 * (I * H // 2 + I * H // 32)
+    res = {"workload": "MTP drafter routed experts: 5 rows, hidden 5120, 3 stages x 128 experts (I=2304, MXFP4) "
+                       "top-3 (drafter router top-3 over random scores), route weights random",
+           "steps": steps, "us_per_call": us, "mean_unique_experts": U,
+           "hbm_gbps": U * ebytes / (us * 1e-6) / 1e9, "hbm_frac": U * ebytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+           "kernel_us": ktot, "gate_up_gbps": U * gu_bytes / (ktot["gate_up_act"] * 1e-6) / 1e9,
+           "top3_us_per_call": top3_us}
+    log(f"drafter experts: {us:.1f} us/call, U={U:.2f}, HBM {res['hbm_gbps']:.0f} GB/s; kernels " +
+        ", ".join(f"{n} {ktot[n]:.1f}" for n in names) + f"; top-3 {top3_us:.1f} us")
+    del P, table
+    torch.cuda.empty_cache()
+    return res
+
+
 def zipf_route_ids(rng, perms, pool, T, K, s=1.1):
     """[pool][L][T][K] int32: per token K distinct Zipf(s) ranks over 1..E (sequential draws without
     replacement), rank r -> expert perms[l][r-1]."""
@@ -371,6 +444,7 @@ def main():
     ap.add_argument("--stack-steps", type=int, default=1000)
     ap.add_argument("--prefill-steps", type=int, default=50)
     ap.add_argument("--stack-warmup", type=int, default=20)
+    ap.add_argument("--drafter-steps", type=int, default=300)
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -515,6 +589,7 @@ def main():
 
     del P, experts, table, layer_args, ws
     torch.cuda.empty_cache()
+    drafter = bench_drafter(gpu, args.drafter_steps, 10) if args.drafter_steps > 0 else None
     stack = bench_stack(gpu, args.stack_steps, args.stack_warmup) if args.stack_steps > 0 else None
 
     out = {
@@ -537,6 +612,7 @@ def main():
         "accept_top_p": accept_tp,
         "step40": stack,
         "prefill": prefill,
+        "drafter_experts": drafter,
     }
     if stack and accept:  # acceptance time as a fraction of the 40-layer step (target < 3 %)
         out["accept"]["frac_of_step40"] = {m: accept["us_per_step"] * 1e-3 / r["ms_per_step"]

@@ -3,6 +3,7 @@
 #include "moe_kernels.inc"
 #include "moe_layer.inc"
 #include "prefill.inc"
+#include "target_experts.inc"
 #include "verify_stack.inc"
 #include "accept.inc"
 #include "spark_gpu.inc"

@@ -104,6 +104,10 @@ def lib():
                                                   ctypes.c_void_p, ctypes.c_void_p]
         _lib.ds41_spark_sample_gpu_v2.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64,
                                                   ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+        _lib.ds41_target_experts_error.restype = ctypes.c_char_p
+        _lib.ds41_target_experts_error.argtypes = [ctypes.c_void_p]
+        _lib.ds41_target_experts.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
         _lib.ds41_spark_verify_logits_gpu_v2.argtypes = [
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_double,
             ctypes.c_double, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
@@ -451,6 +455,63 @@ class VerifyStack:
             self.close()
         except Exception:
             pass
+
+
+# ---- MTP drafter: routed-expert service and router top-3 -------------------------------
+class TargetExpertsDesc(ctypes.Structure):
+    _fields_ = [("table", ctypes.c_void_p), ("expert_base", ctypes.c_int32), ("hidden", ctypes.c_int32),
+                ("inter", ctypes.c_int32), ("swiglu_limit", ctypes.c_float), ("check_routes", ctypes.c_int32),
+                ("stream", ctypes.c_void_p), ("stage_events", ctypes.c_void_p)]
+
+
+class TargetExperts:
+    """ds41_target_experts_*: the ds41_target_experts_fn service over a device table whose
+    drafter experts of stage s, id e are table[expert_base + 128 * s + e]. Calls must use
+    the stream given here. call() raises with the library's error text on failure."""
+
+    def __init__(self, table, expert_base, hidden, inter, swiglu_limit=10.0, check_routes=False, stream=None,
+                 events=None):
+        self.stream = _stream(stream)
+        self.desc = TargetExpertsDesc(table.data_ptr(), expert_base, hidden, inter, swiglu_limit,
+                                      1 if check_routes else 0, self.stream, 0 if events is None else events)
+        self.handle = ctypes.c_void_p(0)
+        check(lib().ds41_target_experts_create(ctypes.byref(self.desc), ctypes.byref(self.handle)),
+              "ds41_target_experts_create")
+        self.H = hidden
+
+    def call_rc(self, stage, x, ids, weights, out, rows=None, stream=None):
+        rows = x.shape[0] if rows is None else rows
+        return lib().ds41_target_experts(self.handle, stage, _p(x), _p(ids), _p(weights), _p(out), rows,
+                                         self.stream if stream is None else _stream(stream))
+
+    def error(self):
+        return lib().ds41_target_experts_error(self.handle).decode()
+
+    def __call__(self, stage, x, ids, weights, out=None):
+        import torch
+        if out is None:
+            out = torch.empty((x.shape[0], 3, self.H), dtype=torch.bfloat16, device=x.device)
+        if self.call_rc(stage, x, ids, weights, out) != 0:
+            raise RuntimeError(f"ds41_target_experts: {self.error()}")
+        return out
+
+    def close(self):
+        if self.handle:
+            lib().ds41_target_experts_destroy(self.handle)
+            self.handle = ctypes.c_void_p(0)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def spark_topk3(scores, stream=None):
+    import torch
+    ids = torch.empty((scores.shape[0], 3), dtype=torch.int32, device=scores.device)
+    check(lib().ds41_spark_topk3_gpu(_p(scores), _p(ids), scores.shape[0], _stream(stream)), "ds41_spark_topk3_gpu")
+    return ids
 
 
 # ---- chunked verify / prefill ---------------------------------------------------------

@@ -295,6 +295,43 @@ int ds41_verify_stack_destroy(void *stack);
 int ds41_host_alloc(size_t bytes, void **out);
 int ds41_host_free(void *p);
 
+/* ---- MTP drafter: routed-expert service and router top-3 -------------------- */
+/* The reference's ds41_target_experts_fn service (engine/include/ds41/target_shared.h:28-39),
+ * bound by Native::services (engine/src/forward.cu:555-566) to routed_spark
+ * (forward.cu:1000-1097). The drafter's routed experts of stage s (logical layer 40 + s,
+ * components/moe/include/ds41/store.hpp:16) are table[expert_base + 128 * s + id],
+ * id 0..127. */
+typedef struct ds41_target_experts_desc {
+  const ds41_device_expert *table; /* device; every drafter expert resident in HBM */
+  int32_t expert_base;             /* table index of stage 0, expert 0 */
+  int32_t hidden, inter;           /* 5120, 2304 for the drafter */
+  float swiglu_limit;              /* 10 (forward.cu:1081) */
+  int32_t check_routes;            /* 1: read the ids back and reject invalid or duplicate
+                                      routes on the host, as the reference does (one stream
+                                      sync per call). 0: the device plan checks them: a
+                                      rejected call writes NaN to every output slot and sets
+                                      status bit 4 (ds41_take_status), without a host wait. */
+  void *stream;                    /* every call must pass this stream (forward.cu:1003) */
+  void *const *stage_events;       /* optional: 8 hipEvent_t, start/stop of the quantise,
+                                      plan, gate/up/act and down kernels */
+} ds41_target_experts_desc;
+/* Allocates the workspace (8 rows x top-3) and, with check_routes, a pinned id buffer. */
+int ds41_target_experts_create(const ds41_target_experts_desc *desc, void **user);
+int ds41_target_experts_destroy(void *user);
+/* ds41_target_experts_fn: x BF16 [rows][hidden] (rows 1..8), ids int32 [rows][3],
+ * weights F32 [rows][3] (all device) -> out BF16 [rows][3][hidden] in top-k slot order,
+ * routed experts only. Returns 0, or -1 with ds41_target_experts_error() set; a failure
+ * poisons the handle and every later call fails (forward.cu:984-998 service_call). */
+int ds41_target_experts(void *user, int stage, const void *x_bf16, const int32_t *ids,
+                        const float *weights, void *out_bf16, int rows, void *stream);
+/* The last call's error, "" after a success; valid until the next call. */
+const char *ds41_target_experts_error(void *user);
+/* The drafter's default router top-3 (engine/third_party/spark/src/forward.cu:28-40
+ * select3, exported at :154 and spark.h:84): scores F32 [rows][128] -> ids int32 [rows][3]
+ * in the tie order of CUDA torch.topk(k=3, sorted=True); rows == 1 sorts with the
+ * 4-entry network and rows > 1 with the 32-entry one, as the reference does. */
+int ds41_spark_topk3_gpu(const float *scores, int32_t *ids, int rows, void *stream);
+
 /* MXFP4 dequantisation: w [n][k/2] + s [n][k/32] -> fp32 [n][k] (bit-exact). */
 int ds41_dequant_mxfp4(const uint8_t *w, const uint8_t *s, float *out, int n, int k,
                        void *stream);

@@ -85,6 +85,15 @@ void oracle_router_scores(const float *logits, const float *bias, int m, int n, 
 /* Top-k per row by biased score, descending, ties -> lower id
  * (engine/src/hotpath/batch.inc:228-237 partial_sort comparator). ids [m][k]. */
 void oracle_topk(const float *b, int m, int n, int k, int32_t *ids);
+/* The MTP drafter's router top-3 (engine/third_party/spark/src/forward.cu:28-40 select3):
+ * scores [m][128] -> ids [m][3]. Pick 3 ids by an upward scan that keeps the first strict
+ * maximum; gather the scores above the third pick's score in id order, then the equal ones
+ * in id order (3 at most); sort with the bitonic network of 4 entries (m == 1) or 32
+ * (m > 1) whose comparator exchanges equal valid pairs.
+ * Pinning: distinct scores give the descending top-3 (closed form); the tie order is pinned
+ * to the reference's own statement that the 32-entry network reverses a tied pair above
+ * the threshold (forward.cu:30-33) and otherwise restated (parity unpinned against torch). */
+void oracle_spark_topk3(const float *scores, int m, int32_t *ids);
 /* engine/src/ops.cu:59-73 route (== components/dense/src/ops.cu:107 routerweights):
  * k=6: sum = ((s0+s4)+s2) + ((s1+s5)+s3); k=3: sum = (s0+s2)+s1; other k: the same
  * four-accumulator rule. w_i = fp32(fp32(s_i / fp32(sum + 1e-20)) * scale). */

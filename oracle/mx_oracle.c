@@ -246,6 +246,59 @@ void oracle_topk(const float *b, int m, int n, int k, int32_t *ids) {
   }
 }
 
+/* Compare-exchange of the drafter's top-3 network: the test is "a is a valid
+ * entry with a strictly larger value, or b is padding"; the pair is exchanged
+ * when the test equals the stage direction. */
+static void top3_cex(float *v, int32_t *id, int *ok, int a, int b, int dir) {
+  const int test = (v[a] > v[b] && ok[a]) || !ok[b];
+  if (test != dir) return;
+  float fv = v[a]; v[a] = v[b]; v[b] = fv;
+  int32_t fi = id[a]; id[a] = id[b]; id[b] = fi;
+  int fo = ok[a]; ok[a] = ok[b]; ok[b] = fo;
+}
+
+void oracle_spark_topk3(const float *scores, int m, int32_t *ids) {
+  const int n = 128, width = m == 1 ? 4 : 32;
+  for (int r = 0; r < m; ++r) {
+    const float *s = scores + (size_t)r * n;
+    int pick[3];
+    for (int k = 0; k < 3; ++k) { /* scan upward; replace only by a strictly larger score */
+      int best = -1;
+      for (int i = 0; i < n; ++i) {
+        int taken = 0;
+        for (int j = 0; j < k; ++j) taken |= pick[j] == i;
+        if (taken) continue;
+        if (best < 0 || s[i] > s[best]) best = i;
+      }
+      pick[k] = best;
+    }
+    const float thr = s[pick[2]];
+    float v[32];
+    int32_t id[32];
+    int ok[32];
+    for (int i = 0; i < 32; ++i) { v[i] = 0.0f; id[i] = 0; ok[i] = i < 3; }
+    int got = 0;
+    for (int i = 0; i < n; ++i)
+      if (s[i] > thr) { v[got] = s[i]; id[got++] = i; }
+    for (int i = 0; i < n && got < 3; ++i)
+      if (s[i] == thr) { v[got] = s[i]; id[got++] = i; }
+    /* bitonic network over `width` entries: pair p of a stage with half-span h
+     * joins entries lo = 2p - (p mod h) and lo + h */
+    for (int size = 2; size < width; size *= 2)
+      for (int h = size / 2; h >= 1; h /= 2)
+        for (int p = 0; p < width / 2; ++p) {
+          const int lo = 2 * p - (p & (h - 1));
+          top3_cex(v, id, ok, lo, lo + h, (p & (size / 2)) != 0);
+        }
+    for (int h = width / 2; h >= 1; h /= 2)
+      for (int p = 0; p < width / 2; ++p) {
+        const int lo = 2 * p - (p & (h - 1));
+        top3_cex(v, id, ok, lo, lo + h, 0);
+      }
+    for (int k = 0; k < 3; ++k) ids[(size_t)r * 3 + k] = id[k];
+  }
+}
+
 void oracle_route_weights(const float *u, const int32_t *ids, int m, int n, int k, float scale,
                           float *w) {
   for (int r = 0; r < m; ++r) {

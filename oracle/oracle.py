@@ -190,6 +190,16 @@ def topk(b, k):
     return ids
 
 
+def spark_topk3(scores):
+    """Drafter router top-3 with CUDA torch.topk's tie order (spark forward.cu:28-40)."""
+    s = np.ascontiguousarray(scores, np.float32)
+    m = s.shape[0]
+    assert s.shape[1] == 128
+    ids = np.empty((m, 3), np.int32)
+    lib().oracle_spark_topk3(_ptr(s), m, _ptr(ids))
+    return ids
+
+
 def route_weights(u, ids, scale=1.5):
     u = np.ascontiguousarray(u, np.float32)
     ids = np.ascontiguousarray(ids, np.int32)

@@ -71,3 +71,22 @@ def test_stack_abi_host_checks():
     assert lib.ds41_verify_stack_create(ctypes.byref(desc), ctypes.byref(h)) == 1
     assert lib.ds41_verify_stack_step(None, None, None, 1, None, None, None, None, None) == 1
     assert lib.ds41_verify_stack_destroy(None) == 1
+
+
+def test_target_experts_abi_host_checks():
+    """Drafter service descriptor layout and the checks that run before any device call."""
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "deepseek-v4.1-flash-pro6000_amd"))
+    import ds41_gfx950 as G
+    assert ctypes.sizeof(G.TargetExpertsDesc) == 48
+    lib = ctypes.CDLL(LIB)
+    h = ctypes.c_void_p(0)
+    d = G.TargetExpertsDesc(0, 0, 5120, 2304, 10.0, 0, None, None)  # null table
+    assert lib.ds41_target_experts_create(ctypes.byref(d), ctypes.byref(h)) == 1 and not h.value
+    d = G.TargetExpertsDesc(64, 0, 5000, 2304, 10.0, 0, None, None)  # hidden not a multiple of 256
+    assert lib.ds41_target_experts_create(ctypes.byref(d), ctypes.byref(h)) == 1 and not h.value
+    lib.ds41_target_experts_error.restype = ctypes.c_char_p
+    assert lib.ds41_target_experts_error(None) == b"null target experts handle"
+    assert lib.ds41_target_experts(None, 0, None, None, None, None, 1, None) == -1
+    assert lib.ds41_target_experts_destroy(None) == 1
+    assert lib.ds41_spark_topk3_gpu(None, None, 1, None) == 1

@@ -228,3 +228,33 @@ def test_swiglu_formula():
     diff = np.abs(O.bf16_to_f32(out) - O.bf16_to_f32(O.bf16_bits(ref)))
     assert np.mean(diff == 0) > 0.99
     assert np.all(diff <= np.abs(O.bf16_to_f32(out)) * 2 ** -7)
+
+
+def test_spark_topk3_distinct_is_descending_top3():
+    """Distinct scores: the drafter's top-3 is the three largest, largest first, for one row
+    (4-entry network) and for several rows (32-entry network)."""
+    rng = np.random.default_rng(41)
+    for m in (1, 5):
+        s = rng.permutation(np.arange(m * 128, dtype=np.float32)).reshape(m, 128) * np.float32(0.37) - 9.0
+        want = np.argsort(-s, axis=1, kind="stable")[:, :3].astype(np.int32)
+        assert np.array_equal(O.spark_topk3(s), want)
+
+
+def test_spark_topk3_tie_orders():
+    """The reference states (spark forward.cu:30-33) that the several-row network reverses a
+    tied pair above the threshold; the one-row network keeps gather order for it. Equal
+    values never change the chosen multiset of scores."""
+    s = np.zeros((1, 128), np.float32)
+    s[0, 10] = s[0, 20] = 5.0
+    s[0, 30] = 1.0
+    assert O.spark_topk3(s).tolist() == [[10, 20, 30]]
+    assert O.spark_topk3(np.repeat(s, 3, 0)).tolist() == [[20, 10, 30]] * 3
+    rng = np.random.default_rng(42)
+    for m in (1, 2, 7):
+        s = rng.integers(0, 4, (m, 128)).astype(np.float32)
+        ids = O.spark_topk3(s)
+        for r in range(m):
+            vals = s[r, ids[r]]
+            assert len(set(ids[r].tolist())) == 3
+            assert np.all(vals[:-1] >= vals[1:])
+            assert sorted(vals.tolist()) == sorted(np.sort(s[r])[-3:].tolist())
