@@ -334,7 +334,21 @@ def zipf_route_ids(rng, perms, pool, T, K, s=1.1):
     return out
 
 
-def bench_stack(gpu, steps, warmup, seed=4):
+def zipf_route_ids_fast(rng, perms, n, T, K, s=1.1):
+    """As zipf_route_ids for n fresh step sets, vectorised: the top-K of log p + Gumbel noise is a
+    sample of K distinct ranks drawn one after another with probability proportional to p."""
+    import numpy as np
+    L, E = len(perms), len(perms[0])
+    logp = -s * np.log(np.arange(1, E + 1, dtype=np.float64))
+    out = np.empty((n, L, T, K), np.int32)
+    for l in range(L):
+        g = logp + rng.gumbel(size=(n, T, E))
+        ranks = np.argpartition(-g, K - 1, axis=-1)[..., :K]
+        out[:, l] = np.asarray(perms[l])[ranks]
+    return out
+
+
+def bench_stack(gpu, steps, warmup, seed=4, cache_slots=1024):
     """the T=4 verify step through 40 stacked MoE layers (H=4096, I=2880, 384 routed experts
     top-6 + 1 shared, independent seeded weights per layer). Per layer the Zipf(1.1)-hottest 320 experts
     (ranks 1..320 of a seeded per-layer permutation) and the shared expert are HBM-resident; the other 64
@@ -393,19 +407,32 @@ def bench_stack(gpu, steps, warmup, seed=4):
     rids = torch.from_numpy(zipf_route_ids(rng, perms, pool, T, K)).to(gpu)
     y = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
     stream = torch.cuda.current_stream()
+    fresh = torch.from_numpy(zipf_route_ids_fast(rng, perms, steps + warmup, T, K)).to(gpu)
     results = {}
-    for mode in ("router", "zipf"):
+    for mode in ("router", "zipf", "zipf_fresh", "zipf_fresh_cache", "router_cache"):
+        if mode == "zipf_fresh_cache":
+            stack.cache(cache_slots)
+            log(f"stack: HBM cache of {cache_slots} slots ({cache_slots * slab / 1e9:.1f} GB), "
+                f"HBM in use {torch.cuda.memory_allocated() / 1e9:.1f} GB + cache")
+
         def step(i):
-            stack.step(xs[i % pool], y, route_ids=rids[i % pool] if mode == "zipf" else None, stream=stream)
+            if mode.startswith("zipf_fresh"):
+                r = fresh[i]
+            elif mode == "zipf":
+                r = rids[i % pool]
+            else:
+                r = None
+            stack.step(xs[i % pool], y, route_ids=r, stream=stream)
         for i in range(warmup):
             step(i)
         torch.cuda.synchronize()
         s0 = stack.stats()
+        c0 = stack.cache_stats() if mode.endswith("cache") else None
         ev = G.Events(2)
         ev.record(0, stream)
         w0 = time.perf_counter()
         for i in range(steps):
-            step(i)
+            step(warmup + i)  # fresh routes: the timed steps never repeat the warmup's
         ev.record(1, stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - w0
@@ -416,14 +443,27 @@ def bench_stack(gpu, steps, warmup, seed=4):
             raise AssertionError(f"stack {mode}: invalid routes or kernel status during the timed steps")
         hbm = (d["resident_routed"] + d["layers"]) * EXPERT_BYTES + d["layers"] * E * H * 4
         sec = ms * 1e-3 * steps
+        routing = {"router": "router on chained activations (4a)",
+                   "zipf": "Zipf(1.1) ids (4b), a pool of 16 step sets",
+                   "zipf_fresh": "Zipf(1.1) ids drawn fresh every step",
+                   "zipf_fresh_cache": f"Zipf(1.1) ids drawn fresh every step, HBM LFU cache of {cache_slots} slots",
+                   "router_cache": f"router on chained activations, HBM LFU cache of {cache_slots} slots"}[mode]
         results[mode] = {
-            "routing": "router on chained activations (4a)" if mode == "router" else "Zipf(1.1) ids (4b)",
+            "routing": routing,
             "steps": steps, "ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / steps,
             "tokens_per_s": T / (ms * 1e-3),
             "hbm_bytes_per_step": hbm / steps, "hbm_gbps": hbm / sec / 1e9, "hbm_frac": hbm / sec / 1e9 / PEAK_HBM_GBPS,
             "h2d_bytes_per_step": d["h2d_bytes"] / steps, "h2d_gbps": d["h2d_bytes"] / sec / 1e9,
             "resident_routed_per_layer": d["resident_routed"] / d["layers"],
             "host_fetched_per_layer": d["host_fetched"] / d["layers"]}
+        if c0 is not None:
+            c1 = stack.cache_stats()
+            cd = {k: c1[k] - c0[k] for k in c1}
+            results[mode]["cache"] = {"slots": cache_slots, "requests": cd["requests"], "hits": cd["hits"],
+                                      "misses": cd["misses"], "evictions": cd["evictions"],
+                                      "hit_rate": cd["hits"] / max(cd["requests"], 1)}
+            log(f"stack {mode}: cache hit rate {cd['hits'] / max(cd['requests'], 1):.3f} "
+                f"({cd['hits']} of {cd['requests']}), evictions {cd['evictions']}")
         log(f"stack {mode}: {ms:.3f} ms/step ({T / (ms * 1e-3):.0f} tok/s), HBM {hbm / sec / 1e9:.0f} GB/s, "
             f"H2D {d['h2d_bytes'] / sec / 1e9:.1f} GB/s, per layer: resident {d['resident_routed'] / d['layers']:.2f}"
             f" host {d['host_fetched'] / d['layers']:.2f}")
@@ -445,6 +485,7 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=50)
     ap.add_argument("--stack-warmup", type=int, default=20)
     ap.add_argument("--drafter-steps", type=int, default=300)
+    ap.add_argument("--stack-cache-slots", type=int, default=1024)
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -590,7 +631,8 @@ def main():
     del P, experts, table, layer_args, ws
     torch.cuda.empty_cache()
     drafter = bench_drafter(gpu, args.drafter_steps, 10) if args.drafter_steps > 0 else None
-    stack = bench_stack(gpu, args.stack_steps, args.stack_warmup) if args.stack_steps > 0 else None
+    stack = bench_stack(gpu, args.stack_steps, args.stack_warmup, cache_slots=args.stack_cache_slots) \
+        if args.stack_steps > 0 else None
 
     out = {
         "metric": METRIC, "value": T / (ms_per_step * 1e-3), "unit": "tokens/s", "n_gpus": 1,

@@ -4,6 +4,7 @@
 #include "moe_layer.inc"
 #include "prefill.inc"
 #include "target_experts.inc"
+#include "expert_pool.inc"
 #include "verify_stack.inc"
 #include "accept.inc"
 #include "spark_gpu.inc"

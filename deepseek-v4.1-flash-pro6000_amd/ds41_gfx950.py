@@ -104,6 +104,11 @@ def lib():
                                                   ctypes.c_void_p, ctypes.c_void_p]
         _lib.ds41_spark_sample_gpu_v2.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64,
                                                   ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+        _lib.ds41_pool_error.restype = ctypes.c_char_p
+        _lib.ds41_pool_error.argtypes = [ctypes.c_void_p]
+        _lib.ds41_placement_load.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                             ctypes.c_char_p, ctypes.c_size_t]
         _lib.ds41_target_experts_error.restype = ctypes.c_char_p
         _lib.ds41_target_experts_error.argtypes = [ctypes.c_void_p]
         _lib.ds41_target_experts.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
@@ -407,6 +412,11 @@ class HostSlabs:
             pass
 
 
+class CacheStats(ctypes.Structure):
+    _fields_ = [("requests", ctypes.c_uint64), ("hits", ctypes.c_uint64), ("misses", ctypes.c_uint64),
+                ("evictions", ctypes.c_uint64), ("h2d_bytes", ctypes.c_uint64)]
+
+
 class VerifyStack:
     """ds41_verify_stack_*: layers is a list of dicts with router_w, router_bias, table (device tensors),
     expert_base, shared_index and optionally host_index (device int32 [E]) + host_slabs (pinned uint8
@@ -440,6 +450,16 @@ class VerifyStack:
         check(lib().ds41_verify_stack_layer(self.handle, l, _p(x), _p(y), x.shape[0], _p(route_ids), _p(ids_out),
                                             _p(weights_out), _stream(stream)), "ds41_verify_stack_layer")
 
+    def cache(self, slots, placement=None):
+        """ds41_verify_stack_cache: an HBM cache of `slots` expert slabs for the host-tier experts."""
+        check(lib().ds41_verify_stack_cache(self.handle, slots, None if placement is None else ctypes.byref(placement)),
+              "ds41_verify_stack_cache")
+
+    def cache_stats(self):
+        st = CacheStats()
+        check(lib().ds41_verify_stack_cache_stats(self.handle, ctypes.byref(st)), "ds41_verify_stack_cache_stats")
+        return {f: int(getattr(st, f)) for f, _ in CacheStats._fields_}
+
     def stats(self):
         st = StackStats()
         check(lib().ds41_verify_stack_stats(self.handle, ctypes.byref(st)), "ds41_verify_stack_stats")
@@ -453,6 +473,114 @@ class VerifyStack:
     def __del__(self):
         try:
             self.close()
+        except Exception:
+            pass
+
+
+# ---- expert slot pool (LFU residency) and placement files -------------------------------
+POOL_MAX_LAYERS = 64
+REFERENCE_LAYERS = [384] * 40 + [128] * 3  # components/moe/include/ds41/store.hpp:16
+
+
+class Placement(ctypes.Structure):
+    _fields_ = [("recent_window", ctypes.c_uint32), ("decay_interval", ctypes.c_uint32),
+                ("distinct_lfu", ctypes.c_int32), ("hard_budgets", ctypes.c_int32),
+                ("layers", ctypes.c_int32), ("n_vram", ctypes.c_int32), ("n_host", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("budget", ctypes.c_uint32 * POOL_MAX_LAYERS),
+                ("host_budget", ctypes.c_uint32 * POOL_MAX_LAYERS), ("vram_pins", ctypes.c_void_p),
+                ("host_residents", ctypes.c_void_p)]
+
+
+class PoolAllocation(ctypes.Structure):
+    _fields_ = [("id", ctypes.c_uint32), ("slot", ctypes.c_int32), ("hit", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("evicted", ctypes.c_int64)]
+
+
+def _u32(ids):
+    arr = (ctypes.c_uint32 * max(len(ids), 1))(*[int(i) & 0xFFFFFFFF for i in ids])
+    return arr
+
+
+def make_placement(layers, budget=None, hard=False, recent=6, decay=32, distinct=True, pins=()):
+    p = Placement()
+    p.recent_window, p.decay_interval, p.distinct_lfu, p.hard_budgets = recent, decay, int(distinct), int(hard)
+    p.layers = layers
+    for l, b in enumerate(budget or []):
+        p.budget[l] = b
+    p._pins = _u32(list(pins))
+    p.n_vram = len(pins)
+    p.vram_pins = ctypes.cast(p._pins, ctypes.c_void_p).value if pins else None
+    return p
+
+
+def load_placement(path, layer_experts=REFERENCE_LAYERS, cap=1 << 16):
+    """ds41_placement_load -> (Placement, vram pins list, host residents list). Raises with the reason."""
+    sizes = _u32(layer_experts)
+    out = Placement()
+    vram, host = (ctypes.c_uint32 * cap)(), (ctypes.c_uint32 * cap)()
+    err = ctypes.create_string_buffer(256)
+    rc = lib().ds41_placement_load(path.encode(), len(layer_experts), sizes, ctypes.byref(out), vram, cap, host, cap,
+                                   err, 256)
+    if rc != 0:
+        raise ValueError(f"ds41_placement_load ({rc}): {err.value.decode()}")
+    out._keep = (vram, host)
+    return out, list(vram[:out.n_vram]), list(host[:out.n_host])
+
+
+class ExpertPool:
+    """ds41_pool_*: the library's expert slot pool. Methods return what the C calls return;
+    acquire/borrow give (rc, [(id, slot, hit, evicted), ...])."""
+
+    def __init__(self, slots, layer_experts=REFERENCE_LAYERS, recent=6, decay=32, distinct=True):
+        self.h = ctypes.c_void_p(0)
+        sizes = _u32(layer_experts)
+        rc = lib().ds41_pool_create(slots, len(layer_experts), sizes, recent, decay, int(distinct),
+                                    ctypes.byref(self.h))
+        if rc != 0:
+            raise ValueError(f"ds41_pool_create failed ({rc})")
+
+    def _allocs(self, fn, ids, *extra):
+        out = (PoolAllocation * max(len(ids), 1))()
+        rc = fn(self.h, _u32(ids), len(ids), *extra, out)
+        return rc, [(a.id, a.slot, bool(a.hit), a.evicted) for a in out[:max(rc, 0)]]
+
+    def acquire(self, ids, prefetch=False):
+        return self._allocs(lib().ds41_pool_acquire, ids, int(prefetch))
+
+    def borrow(self, ids):
+        return self._allocs(lib().ds41_pool_borrow, ids)
+
+    def release(self, lease):
+        arr = (PoolAllocation * max(len(lease), 1))()
+        for i, (e, s, h, ev) in enumerate(lease):
+            arr[i].id, arr[i].slot, arr[i].hit, arr[i].evicted = e, s, int(h), ev
+        return lib().ds41_pool_release(self.h, arr, len(lease))
+
+    def touch(self, ids):
+        return lib().ds41_pool_touch(self.h, _u32(ids), len(ids))
+
+    def policy(self, placement):
+        return lib().ds41_pool_policy(self.h, ctypes.byref(placement))
+
+    def pin(self, e):
+        return lib().ds41_pool_pin(self.h, ctypes.c_uint32(e))
+
+    def unpin(self, e):
+        return lib().ds41_pool_unpin(self.h, ctypes.c_uint32(e))
+
+    def residency(self, e):
+        return lib().ds41_pool_residency(self.h, ctypes.c_uint32(e))
+
+    def reset_history(self):
+        return lib().ds41_pool_reset_history(self.h)
+
+    def error(self):
+        return lib().ds41_pool_error(self.h).decode()
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().ds41_pool_destroy(self.h)
         except Exception:
             pass
 

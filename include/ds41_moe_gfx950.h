@@ -287,6 +287,7 @@ int ds41_verify_stack_layer(void *stack, int layer, const void *x_bf16, void *y_
                             const int32_t *route_ids, int32_t *ids_out, float *weights_out,
                             void *stream);
 int ds41_verify_stack_stats(void *stack, ds41_stack_stats *out);
+
 int ds41_verify_stack_destroy(void *stack);
 /* Pinned host memory for host-tier slabs (the reference's HostBuffer,
  * components/moe/include/ds41/store.hpp:161-174, which registers an existing
@@ -294,6 +295,73 @@ int ds41_verify_stack_destroy(void *stack);
  * copies from them run asynchronously). Synchronous; *out is NULL on error. */
 int ds41_host_alloc(size_t bytes, void **out);
 int ds41_host_free(void *p);
+
+/* ---- expert slot pool (LFU residency policy) and placement files ------------- */
+/* The reference's SlotPool (components/moe/include/ds41/store.hpp:80-157, store.cpp:15-196): a
+ * CPU-only, deterministic assignment of experts to HBM slots. Expert ids are flattened layer by
+ * layer: layer l owns ids first(l) .. first(l) + layer_experts[l] - 1 (the reference's space is
+ * 40 layers of 384 then 3 of 128, store.hpp:16). Errors: -1 capacity (the need set exceeds the
+ * usable slots), -2 id out of range, -3 illegal state (bad release, pin of a non-resident
+ * expert), -4 invalid argument; ds41_pool_error() gives the text. No call touches the GPU. */
+#define DS41_POOL_MAX_LAYERS 64
+typedef struct ds41_placement {      /* Placement, store.hpp:39-47 */
+  uint32_t recent_window, decay_interval;
+  int32_t distinct_lfu, hard_budgets;
+  int32_t layers, n_vram, n_host, reserved;
+  uint32_t budget[DS41_POOL_MAX_LAYERS];      /* dynamic slots per layer, pins excluded */
+  uint32_t host_budget[DS41_POOL_MAX_LAYERS];
+  const uint32_t *vram_pins;          /* [n_vram] */
+  const uint32_t *host_residents;     /* [n_host] */
+} ds41_placement;
+/* load_placement (components/moe/src/manifest.cpp:8-34): the text format of the reference's
+ * profiles/p80-mtp48.placement. The id lists are written to the caller's arrays. Returns 0 or a
+ * negative code with the reason in `error`. */
+int ds41_placement_load(const char *path, int layers, const uint32_t *layer_experts,
+                        ds41_placement *out, uint32_t *vram_pins, int vram_cap,
+                        uint32_t *host_residents, int host_cap, char *error, size_t error_bytes);
+typedef struct ds41_pool_allocation { /* SlotPool::Allocation */
+  uint32_t id;
+  int32_t slot;
+  int32_t hit;
+  int32_t reserved;
+  int64_t evicted;                    /* expert id that lost the slot, -1 for none */
+} ds41_pool_allocation;
+/* SlotPool(slots, recent_window, decay_interval, distinct_lfu) */
+int ds41_pool_create(int slots, int layers, const uint32_t *layer_experts, uint32_t recent_window,
+                     uint32_t decay_interval, int distinct_lfu, void **pool);
+int ds41_pool_destroy(void *pool);
+const char *ds41_pool_error(void *pool);
+int ds41_pool_policy(void *pool, const ds41_placement *placement);   /* SlotPool::policy */
+/* SlotPool::acquire: one allocation per distinct id in first-seen order (out may be NULL);
+ * returns their count. prefetch != 0 leaves the LFU history alone. */
+int ds41_pool_acquire(void *pool, const uint32_t *ids, int n, int prefetch,
+                      ds41_pool_allocation *out);
+int ds41_pool_borrow(void *pool, const uint32_t *ids, int n, ds41_pool_allocation *out);
+/* SlotPool::release. A lease listing one slot more often than it is leased is rejected. */
+int ds41_pool_release(void *pool, const ds41_pool_allocation *lease, int n);
+int ds41_pool_touch(void *pool, const uint32_t *ids, int n);
+int ds41_pool_pin(void *pool, uint32_t id);
+int ds41_pool_unpin(void *pool, uint32_t id);
+int ds41_pool_residency(void *pool, uint32_t id);                     /* slot or -1 */
+int ds41_pool_reset_history(void *pool);
+
+/* Dynamic HBM cache for the stack's host-tier experts, the reference's VRAM slot pool in front
+ * of its host tier (components/moe/src/offload.cpp:240-381 load, SlotPool policy store.cpp).
+ * Allocates `slots` expert slabs in HBM (slots >= max_tokens * topk), a pinned patch buffer and
+ * one event per layer; call before the first step or between steps. A routed host-tier expert
+ * that the pool holds is read in place (a hit); a miss is copied from its host slab into the
+ * slot the policy assigns, after the copy stream has waited for the last layer that read the
+ * slot's previous expert. `policy` (nullable: recent 6, decay 32, distinct, soft, no budgets)
+ * applies its recent/decay/lfu/pools/budget fields to the stack's layers (policy->layers must
+ * equal the stack's); its pin and host lists are not used, because the stack's resident
+ * experts come from each layer's table. Expert id of layer l, expert e: l * n_experts + e. */
+int ds41_verify_stack_cache(void *stack, int slots, const ds41_placement *policy);
+typedef struct ds41_cache_stats {
+  uint64_t requests;                 /* routed host-tier experts served through the cache */
+  uint64_t hits, misses, evictions;
+  uint64_t h2d_bytes;
+} ds41_cache_stats;
+int ds41_verify_stack_cache_stats(void *stack, ds41_cache_stats *out);
 
 /* ---- MTP drafter: routed-expert service and router top-3 -------------------- */
 /* The reference's ds41_target_experts_fn service (engine/include/ds41/target_shared.h:28-39),

@@ -82,6 +82,34 @@ def ref():
     return _ref
 
 
+REFPOOL_PATH = os.path.join(HERE, "_ref", "libds41_refpool.so")
+_refpool = None
+
+
+def refpool():
+    """The reference's SlotPool and placement parser (components/moe/src/store.cpp, manifest.cpp)
+    behind oracle/refpool_shim.cpp, compiled from the reference sources by `make -C oracle ref`.
+    None when it was not built."""
+    global _refpool
+    if _refpool is None and os.path.exists(REFPOOL_PATH):
+        R = ctypes.CDLL(REFPOOL_PATH)
+        R.refpool_create.restype = ctypes.c_void_p
+        R.refpool_create.argtypes = [ctypes.c_size_t, ctypes.c_uint, ctypes.c_uint, ctypes.c_int]
+        for f in ("refpool_destroy", "refpool_reset"):
+            getattr(R, f).argtypes = [ctypes.c_void_p]
+        R.refpool_policy.argtypes = [ctypes.c_void_p, P, ctypes.c_int, P, ctypes.c_int, ctypes.c_uint, ctypes.c_uint,
+                                     ctypes.c_int]
+        R.refpool_acquire.argtypes = [ctypes.c_void_p, P, ctypes.c_int, ctypes.c_int, P]
+        R.refpool_borrow.argtypes = [ctypes.c_void_p, P, ctypes.c_int, P]
+        R.refpool_release.argtypes = [ctypes.c_void_p, P, ctypes.c_int]
+        R.refpool_touch.argtypes = [ctypes.c_void_p, P, ctypes.c_int]
+        for f in ("refpool_pin", "refpool_unpin", "refpool_residency"):
+            getattr(R, f).argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+        R.refplacement_load.argtypes = [ctypes.c_char_p, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
+        _refpool = R
+    return _refpool
+
+
 def _ptr(a):
     return ctypes.c_void_p(a.ctypes.data) if a is not None else ctypes.c_void_p(0)
 

@@ -217,3 +217,63 @@ def test_stack_layer_entry_matches_step(gpu):
         torch.cuda.synchronize()
         assert np.array_equal(host(i), ids[l])
         assert np.array_equal(host(cur).view(np.uint8), (y if l == L - 1 else lo[l]).view(np.uint8))
+
+
+def host_demands(ids, host_sets, E):
+    """Per layer, the host-tier experts the plan hands to the cache: distinct routed ids in the host
+    set, ascending (the plan numbers jobs by expert id), as flattened ids l * E + e."""
+    return [[l * E + e for e in sorted(set(ids[l].ravel().tolist()) & host_sets[l])] for l in range(len(host_sets))]
+
+
+@pytest.mark.parametrize("slots,budget", [(24, None), (40, (10, 18, 12))])
+def test_stack_cache_bitexact_and_policy(gpu, slots, budget):
+    """An HBM cache in front of the host tier (ds41_verify_stack_cache): over 10 steps with fresh
+    host-heavy routes every output equals the all-resident stack's bit for bit, and the hits,
+    misses and evictions equal those of the library's slot pool replaying the same demands."""
+    import torch
+    import ds41_gfx950 as G
+    L, H, I, E, K, T = 3, 512, 256, 32, 6, 4
+    host_sets = [range(l, E, 2) for l in range(L)]  # 16 host-tier experts per layer
+    say(f"stack cache slots={slots} budget={budget} L={L} E={E} T={T}")
+    st = Stack(gpu, 31, L, H, I, E, K, T, host_sets)
+    placement = None
+    if budget is not None:
+        placement = G.make_placement(L, list(budget), recent=2, decay=4)
+    st.tier.cache(slots, placement)
+    model = G.ExpertPool(slots, [E] * L, recent=6 if placement is None else 2, decay=32 if placement is None else 4)
+    if placement is not None:
+        assert model.policy(placement) == 0
+    rng = np.random.default_rng(32)
+    hits = misses = evictions = 0
+    G.take_status()
+    for step in range(10):
+        hs = [sorted(st.host_sets[l]) for l in range(L)]
+        rid = np.empty((L, T, K), np.int32)
+        for l in range(L):
+            for t in range(T):  # mostly host-tier experts, some resident ones
+                pool = hs[l][:10] if step % 2 else hs[l]
+                n_host = int(rng.integers(3, 6))
+                pick = list(rng.choice(pool, n_host, replace=False))
+                rest = [e for e in range(E) if e not in st.host_sets[l]]
+                pick += list(rng.choice(rest, K - n_host, replace=False))
+                rid[l, t] = pick
+        route = torch.from_numpy(rid).to(gpu)
+        x = rand_x(gpu, 40 + step, T, H)
+        a = st.run("tier", x, route)
+        b = st.run("all", x, route)
+        check_same(a, b)
+        for want in host_demands(rid, st.host_sets, E):
+            if not want:
+                continue
+            rc, got = model.acquire(want)
+            assert rc == len(want)
+            hits += sum(g[2] for g in got)
+            misses += sum(not g[2] for g in got)
+            evictions += sum(g[3] >= 0 for g in got)
+            assert model.release(got) == 0
+    assert G.take_status() == 0
+    cs = st.tier.cache_stats()
+    say(f"  cache {cs}")
+    assert cs["hits"] == hits and cs["misses"] == misses and cs["evictions"] == evictions
+    assert cs["requests"] == hits + misses and cs["h2d_bytes"] == misses * st.slab
+    assert hits > 0 and evictions > 0
