@@ -6,5 +6,6 @@
 #include "target_experts.inc"
 #include "expert_pool.inc"
 #include "verify_stack.inc"
+#include "expert_records.inc"
 #include "accept.inc"
 #include "spark_gpu.inc"

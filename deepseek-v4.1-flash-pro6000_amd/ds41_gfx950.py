@@ -585,6 +585,85 @@ class ExpertPool:
             pass
 
 
+# ---- on-disk expert format ----------------------------------------------------------------
+class RecordInfo(ctypes.Structure):
+    _fields_ = [("id", ctypes.c_uint32), ("n_extents", ctypes.c_int32), ("bytes", ctypes.c_uint64),
+                ("view_offset", ctypes.c_uint64 * 6), ("view_bytes", ctypes.c_uint64 * 6)]
+
+
+class RecordExtent(ctypes.Structure):
+    _fields_ = [("path", ctypes.c_char * 4096), ("file_offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64),
+                ("dst_offset", ctypes.c_uint64), ("required_bytes", ctypes.c_uint64),
+                ("expected_file_bytes", ctypes.c_uint64)]
+
+
+class Records:
+    """ds41_records_*: a records manifest (R/E lines) over safetensors shards. Methods raise
+    ValueError with the library's reason."""
+
+    def __init__(self, manifest):
+        self.h = ctypes.c_void_p(0)
+        err = ctypes.create_string_buffer(512)
+        if lib().ds41_records_load(manifest.encode(), ctypes.byref(self.h), err, 512) != 0:
+            raise ValueError(err.value.decode())
+
+    def count(self):
+        return lib().ds41_records_count(self.h)
+
+    def find(self, expert_id):
+        return lib().ds41_records_find(self.h, ctypes.c_uint32(expert_id))
+
+    def info(self, i):
+        o = RecordInfo()
+        if lib().ds41_records_info(self.h, i, ctypes.byref(o)) != 0:
+            raise ValueError("record index")
+        return dict(id=o.id, bytes=o.bytes, n_extents=o.n_extents,
+                    views=[(o.view_offset[k], o.view_bytes[k]) for k in range(6)])
+
+    def extents(self, i):
+        out = []
+        for k in range(self.info(i)["n_extents"]):
+            e = RecordExtent()
+            if lib().ds41_records_extent(self.h, i, k, ctypes.byref(e)) != 0:
+                raise ValueError("extent index")
+            out.append((e.path.decode(), e.file_offset, e.bytes, e.dst_offset, e.required_bytes,
+                        e.expected_file_bytes))
+        return out
+
+    def validate(self, root, complete=True):
+        err = ctypes.create_string_buffer(512)
+        if lib().ds41_records_validate(self.h, root.encode(), int(complete), err, 512) != 0:
+            raise ValueError(err.value.decode())
+
+    def read(self, i):
+        import numpy as np
+        buf = np.zeros(self.info(i)["bytes"], np.uint8)
+        err = ctypes.create_string_buffer(512)
+        if lib().ds41_record_read(self.h, i, ctypes.c_void_p(buf.ctypes.data), buf.size, err, 512) != 0:
+            raise ValueError(err.value.decode())
+        return buf
+
+    def load_slab(self, i, hidden, inter, out=None):
+        """Reads record i and repacks it into a canonical slab (numpy uint8, or `out`: any object
+        with a data_ptr() / numpy array of at least the slab size)."""
+        import numpy as np
+        _, slab = slab_layout(hidden, inter)
+        if out is None:
+            out = np.zeros(slab, np.uint8)
+        ptr = out.data_ptr() if hasattr(out, "data_ptr") else out.ctypes.data
+        err = ctypes.create_string_buffer(512)
+        if lib().ds41_record_load_slab(self.h, i, hidden, inter, ctypes.c_void_p(ptr), slab, err, 512) != 0:
+            raise ValueError(err.value.decode())
+        return out
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().ds41_records_free(self.h)
+        except Exception:
+            pass
+
+
 # ---- MTP drafter: routed-expert service and router top-3 -------------------------------
 class TargetExpertsDesc(ctypes.Structure):
     _fields_ = [("table", ctypes.c_void_p), ("expert_base", ctypes.c_int32), ("hidden", ctypes.c_int32),

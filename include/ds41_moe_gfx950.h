@@ -363,6 +363,50 @@ typedef struct ds41_cache_stats {
 } ds41_cache_stats;
 int ds41_verify_stack_cache_stats(void *stack, ds41_cache_stats *out);
 
+/* ---- on-disk expert format: records manifest over safetensors shards ------------- */
+/* load_records (components/moe/src/manifest.cpp:35-55): the manifest written by the reference's
+ * scripts/assets/expert_bank.py export_tsv. "R id bytes (offset bytes) x 6" gives a record
+ * buffer of `bytes` and six views into it (gate, gate scales, up, up scales, down, down scales =
+ * checkpoint w1/w3/w2 .weight/.scale); "E id "path" file_offset bytes dst_offset required
+ * expected_file_bytes" lines give the file ranges that fill it. Ids as in store.hpp:16.
+ * Calls return 0 or -1 with the reason in `error` (may be NULL). Host code, no device calls. */
+typedef struct ds41_record_info {
+  uint32_t id;
+  int32_t n_extents;
+  uint64_t bytes;
+  uint64_t view_offset[6], view_bytes[6];
+} ds41_record_info;
+typedef struct ds41_record_extent {
+  char path[4096];
+  uint64_t file_offset, bytes, dst_offset;
+  uint64_t required_bytes;          /* 0: all of bytes */
+  uint64_t expected_file_bytes;
+} ds41_record_extent;
+int ds41_records_load(const char *manifest, void **records, char *error, size_t error_bytes);
+int ds41_records_free(void *records);
+int ds41_records_count(void *records);
+int ds41_records_find(void *records, uint32_t id);                   /* index or -1 */
+int ds41_records_info(void *records, int index, ds41_record_info *out);
+int ds41_records_extent(void *records, int index, int extent, ds41_record_extent *out);
+/* The engine's checks before any read (engine/src/forward.cu:1781-1832 validate_records with
+ * engine/src/store.cpp:79-91 validate_spans and the checkpoint index/shard checks of
+ * store.cpp:140-217): every record reads exactly its expert's six tensors of the safetensors
+ * checkpoint under checkpoint_root (model.safetensors.index.json), at their own files and
+ * offsets, within required extent coverage, with no extraneous extent. complete != 0 also
+ * requires every shard file to have its full size. */
+int ds41_records_validate(void *records, const char *checkpoint_root, int complete, char *error,
+                          size_t error_bytes);
+/* Reads a record's extents into dst (>= bytes). A final extent may stop at EOF once its
+ * required bytes have arrived; the rest of it is zeroed. */
+int ds41_record_read(void *records, int index, void *dst, size_t dst_bytes, char *error,
+                     size_t error_bytes);
+/* Repacks a read record into the canonical slab of ds41_expert_slab_layout(hidden, inter); the
+ * views must have the shape's tensor sizes. ds41_record_load_slab = read + repack. */
+int ds41_record_to_slab(void *records, int index, const void *record_buf, int hidden, int inter,
+                        void *slab, size_t slab_bytes, char *error, size_t error_bytes);
+int ds41_record_load_slab(void *records, int index, int hidden, int inter, void *slab,
+                          size_t slab_bytes, char *error, size_t error_bytes);
+
 /* ---- MTP drafter: routed-expert service and router top-3 -------------------- */
 /* The reference's ds41_target_experts_fn service (engine/include/ds41/target_shared.h:28-39),
  * bound by Native::services (engine/src/forward.cu:555-566) to routed_spark

@@ -106,6 +106,7 @@ def refpool():
         for f in ("refpool_pin", "refpool_unpin", "refpool_residency"):
             getattr(R, f).argtypes = [ctypes.c_void_p, ctypes.c_uint32]
         R.refplacement_load.argtypes = [ctypes.c_char_p, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
+        R.refrecords_load.argtypes = [ctypes.c_char_p, ctypes.c_int, P, ctypes.c_int, P, P, P]
         _refpool = R
     return _refpool
 

@@ -1,4 +1,5 @@
-// C entry points over the reference's own SlotPool and placement parser
+// C entry points over the reference's own SlotPool, placement parser and
+// records manifest parser
 // (components/moe/src/store.cpp, manifest.cpp), compiled from the reference
 // sources into oracle/_ref/libds41_refpool.so by `make ref`.
 // TEST INFRASTRUCTURE ONLY: tests/ compare the library's ExpertPool against it.
@@ -113,6 +114,41 @@ int refplacement_load(const char *path, uint32_t *out_u32, uint32_t *budget, uin
     std::memcpy(vram, q.vram_pins.data(), 4 * q.vram_pins.size());
     std::memcpy(host, q.host_residents.data(), 4 * q.host_residents.size());
     return 0;
+  });
+}
+// Records manifest: rec[15] per record = id, bytes, 6 x (offset, bytes), extent count;
+// ext[6] per extent = record index, file_offset, bytes, dst_offset, required, expected;
+// paths 4096 bytes per extent. Returns the record count.
+int refrecords_load(const char *path, int cap, uint64_t *rec, int ecap, uint64_t *ext, char *paths, int *n_ext) {
+  return guarded([&] {
+    const auto r = ds41::load_records(path);
+    if ((int)r.size() > cap) return -1;
+    int k = 0;
+    for (size_t i = 0; i < r.size(); ++i) {
+      uint64_t *o = rec + 15 * i;
+      const ds41::TensorView v[6] = {r[i].gate, r[i].gate_scale, r[i].up, r[i].up_scale, r[i].down, r[i].down_scale};
+      o[0] = r[i].id;
+      o[1] = r[i].bytes;
+      for (int j = 0; j < 6; ++j) {
+        o[2 + 2 * j] = v[j].offset;
+        o[3 + 2 * j] = v[j].bytes;
+      }
+      o[14] = r[i].extents.size();
+      for (const auto &e : r[i].extents) {
+        if (k >= ecap || e.path.size() >= 4096) return -1;
+        uint64_t *x = ext + 6 * k;
+        x[0] = i;
+        x[1] = e.file_offset;
+        x[2] = e.bytes;
+        x[3] = e.dst_offset;
+        x[4] = e.required_bytes;
+        x[5] = e.expected_file_bytes;
+        std::memcpy(paths + 4096 * k, e.path.c_str(), e.path.size() + 1);
+        ++k;
+      }
+    }
+    *n_ext = k;
+    return (int)r.size();
   });
 }
 }
