@@ -3,6 +3,7 @@
 #include "moe_kernels.inc"
 #include "moe_layer.inc"
 #include "prefill.inc"
+#include "dense_fp8.inc"
 #include "target_experts.inc"
 #include "expert_pool.inc"
 #include "verify_stack.inc"

@@ -319,6 +319,108 @@ struct Gemv16 {
   }
 };
 
+// FP8 (E4M3) weights with one E8M0 scale per 32 x 32 block (row block n/32,
+// K32 group g at scale[(n/32) * (k/32) + g]; components/dense/src/dense.cu:37-91),
+// against MXFP8 activation rows from an XTile. B operand of the scaled MFMA in
+// FP8 form (format code 0) has A's layout: lane l holds column l&15, bytes
+// 0..15 = k 16q..16q+15 and 16..31 = k 64+16q..64+16q+15 of the 128-k chunk,
+// q = l>>4, and the E8M0 of K32 block q. All 16 channels of a wave sit in one
+// 32-row scale block, so a lane's scales are bytes q, 4+q, 8+q, ... of that
+// block's scale row: one 16-byte load per batch of 4 chunks gives byte q of
+// dwords 0..3. Two batches of U = 4 chunks are in flight (ping-pong). Pieces at
+// k >= K (the partial last chunk) are zero; their activations are zero too.
+struct Gemv16F8 {
+  static constexpr int U = 4;
+  const uint8_t *w;   // weight row of this lane's channel
+  const uint8_t *sr;  // scale row of the channel's 32-row block
+  int q, k, ng, nch, nb;
+  uint4 A[U][2], B[U][2];
+  uint4 SA, SB;
+
+  __device__ __forceinline__ uint4 piece(int off) const {
+    const int o = off < k ? off : 0;  // clamped address; the value is replaced below
+    const u32x4 v = *(global_u4u)(w + o);
+    return off < k ? make_uint4(v.x, v.y, v.z, v.w) : make_uint4(0, 0, 0, 0);
+  }
+  __device__ __forceinline__ void load(uint4 (*buf)[2], uint4 &S, int b) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int c = b * U + u;
+      c = c < nch ? c : nch - 1;
+      buf[u][0] = piece(128 * c + 16 * q);
+      buf[u][1] = piece(128 * c + 64 + 16 * q);
+    }
+    // scale dwords 4b .. 4b+3 (groups 16b .. 16b+15), clamped to the row
+    int g0 = 16 * b;
+    g0 = g0 + 16 <= ng ? g0 : (ng >= 16 ? ng - 16 : 0);
+    if (ng >= 16) {
+      const u32x4 v = *(global_u4u)(sr + g0);
+      S = make_uint4(v.x, v.y, v.z, v.w);
+    } else {  // short rows (k < 512): bytes clamped to the row, packed four to a dword
+      uint32_t d[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) d[i >> 2] |= (uint32_t)sr[i < ng ? i : ng - 1] << (8 * (i & 3));
+      S = make_uint4(d[0], d[1], d[2], d[3]);
+    }
+  }
+  __device__ __forceinline__ Gemv16F8(const uint8_t *wrow, const uint8_t *srow, int kk) {
+    q = (threadIdx.x & 63) >> 4;
+    w = wrow;
+    sr = srow;
+    k = kk;
+    ng = kk >> 5;
+    nch = (ng + 3) >> 2;
+    nb = (nch + U - 1) / U;
+    load(A, SA, 0);
+  }
+  // scale byte of K32 group 4c + q for chunk u of batch b (S loaded for batch b)
+  __device__ __forceinline__ int scale_of(const uint4 &S, int b, int u) const {
+    const int c = b * U + u, g = 4 * c + q;
+    const int gc = g < ng ? g : ng - 1;
+    int g0 = 16 * b;
+    g0 = g0 + 16 <= ng ? g0 : (ng >= 16 ? ng - 16 : 0);
+    const int idx = gc - g0;  // 0..15 within the loaded window
+    const uint32_t d = (idx >> 2) == 0 ? S.x : (idx >> 2) == 1 ? S.y : (idx >> 2) == 2 ? S.z : S.w;
+    return (int)((d >> (8 * (idx & 3))) & 0xffu);
+  }
+  __device__ __forceinline__ v4f run(const XTile &xt) {
+    const int lane = threadIdx.x & 63, i = lane & 15;
+    const int ii = i < xt.tokens ? i : 0;
+    const uint8_t *xa = xt.q + ii * xt.stride + 16 * q;
+    const uint8_t *sa = xt.s + ii * xt.sstride + q;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const uint4 (*buf)[2], const uint4 &S, int b) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = b * U + u;
+        const int cx = c < nch ? c : nch;  // nch is the zero chunk
+        const uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * cx);
+        const uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * cx + 64);
+        const v8i av = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        const v8i bv = v8i{(int)buf[u][0].x, (int)buf[u][0].y, (int)buf[u][0].z, (int)buf[u][0].w,
+                           (int)buf[u][1].x, (int)buf[u][1].y, (int)buf[u][1].z, (int)buf[u][1].w};
+        acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, 0, 0, 0, (int)sa[4 * cx], 0,
+                                                                scale_of(S, b, u));
+      }
+    };
+    int b = 0;
+    for (; b + 2 < nb; b += 2) {
+      load(B, SB, b + 1);
+      compute(A, SA, b);
+      load(A, SA, b + 2);
+      compute(B, SB, b + 1);
+    }
+    if (b + 2 == nb) {
+      load(B, SB, b + 1);
+      compute(A, SA, b);
+      compute(B, SB, b + 1);
+    } else {
+      compute(A, SA, b);
+    }
+    return acc;
+  }
+};
+
 // Copy `bytes` contiguous bytes global -> LDS with the whole workgroup
 // (16-byte pieces when both ends allow it). Caller syncs.
 __device__ __forceinline__ void stage_bytes(uint8_t *dst, const uint8_t *src, int bytes) {

@@ -42,7 +42,8 @@ class MoeLayerArgs(ctypes.Structure):
                 ("y_bf16", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_size_t), ("ids_out", ctypes.c_void_p),
                 ("weights_out", ctypes.c_void_p), ("logits_out", ctypes.c_void_p),
-                ("stage_events", ctypes.c_void_p), ("stage_mask", ctypes.c_uint32)]
+                ("stage_events", ctypes.c_void_p), ("stage_mask", ctypes.c_uint32),
+                ("shared_fp8", ctypes.c_void_p)]
 
 
 class MoePrefillArgs(ctypes.Structure):
@@ -277,6 +278,45 @@ def make_layer_args(x, router_w, router_bias, table, expert_base, shared_index, 
     a.weights_out = 0 if weights_out is None else weights_out.data_ptr()
     a.logits_out = 0 if logits_out is None else logits_out.data_ptr()
     return a
+
+
+def fp8_expert(e):
+    """Host DeviceExpert for an FP8 shared expert given a dict of device tensors (gate, gate_scale,
+    up, up_scale, down, down_scale); keep the returned object alive while the layer args use it."""
+    d = DeviceExpert()
+    for f in ("gate", "gate_scale", "up", "up_scale", "down", "down_scale"):
+        setattr(d, f, e[f].data_ptr())
+    d.slot = -1
+    return d
+
+
+def dense_quant(x, stream=None):
+    import torch
+    M, K = x.shape
+    a = torch.empty((M, K), dtype=torch.uint8, device=x.device)
+    s = torch.empty((M, K // 32), dtype=torch.uint8, device=x.device)
+    check(lib().ds41_dense_quant(_p(x), _p(a), _p(s), M, K, _stream(stream)), "ds41_dense_quant")
+    return a, s
+
+
+def dense_fp8(a, as_, w, ws, N, variant=-1, stream=None):
+    import torch
+    M, K = a.shape
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    check(lib().ds41_dense_fp8(_p(a), _p(as_), _p(w), _p(ws), _p(y), M, N, K, variant, _stream(stream)),
+          "ds41_dense_fp8")
+    return y
+
+
+def dense_shared_act(g, u, stream=None):
+    import torch
+    M, K = g.shape
+    z = torch.empty_like(g)
+    a = torch.empty((M, K), dtype=torch.uint8, device=g.device)
+    s = torch.empty((M, K // 32), dtype=torch.uint8, device=g.device)
+    check(lib().ds41_dense_shared_act(_p(g), _p(u), _p(z), _p(a), _p(s), M, K, _stream(stream)),
+          "ds41_dense_shared_act")
+    return z, a, s
 
 
 def moe_layer(args, stream=None):

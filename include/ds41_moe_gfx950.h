@@ -146,6 +146,12 @@ typedef struct ds41_moe_layer_args {
                                      reduce) in order (hipExtLaunchKernel) */
   uint32_t stage_mask;            /* 0: every kernel. Otherwise bit i launches kernel i only (for
                                      timing one kernel on a workspace a full call has prepared) */
+  const ds41_device_expert *shared_fp8; /* optional host struct: the shared expert as the checkpoint
+                                     stores it, FP8 E4M3 gate/up [inter][hidden] and down
+                                     [hidden][inter] with one E8M0 scale per 32 x 32 block
+                                     ([rows/32][cols/32]); W8A8 with MXFP8 activations
+                                     (components/dense/src/dense.cu:37-91, batch.inc:330-335
+                                     bshared). Requires shared_index < 0. */
 } ds41_moe_layer_args;
 size_t ds41_moe_layer_workspace_bytes(int tokens, int hidden, int inter, int n_experts,
                                       int topk);
@@ -295,6 +301,21 @@ int ds41_verify_stack_destroy(void *stack);
  * copies from them run asynchronously). Synchronous; *out is NULL on error. */
 int ds41_host_alloc(size_t bytes, void **out);
 int ds41_host_free(void *p);
+
+/* ---- FP8 W8A8 shared-expert projections (components/dense/include/ds41/dense.h) ---- */
+/* ds41_dense_quant (dense.h:10, dense.cu:8-15): MXFP8 quantisation of BF16 rows, the same rule as
+ * ds41_quantize_mxfp8. */
+int ds41_dense_quant(const void *x_bf16, void *a_fp8, void *as_ue8m0, int M, int K, void *stream);
+/* ds41_dense_fp8 (dense.h:11-17, dense.cu:37-91 and 98-106): y BF16 [M][N] = MXFP8 a [M][K] x E4M3
+ * w [N][K] with one E8M0 scale per 32 x 32 block (ws [N/32][K/32]); every K32 block dot times
+ * both scales, added in ascending K in fp32. M <= 8, N and K multiples of 32. `variant` (-1, 0..6)
+ * is accepted for the reference's signature and ignored: one gfx950 kernel serves all shapes. */
+int ds41_dense_fp8(const void *a_fp8, const void *as_ue8m0, const void *w_fp8, const void *ws_ue8m0,
+                   void *y_bf16, int M, int N, int K, int variant, void *stream);
+/* ds41_dense_shared_act (dense.h:41, ops.cu:103-106): z = BF16(SwiGLU(gate, up) with limit 10)
+ * (z may be NULL) and its MXFP8 codes/scales. */
+int ds41_dense_shared_act(const void *gate_bf16, const void *up_bf16, void *z_bf16, void *a_fp8,
+                          void *as_ue8m0, int M, int K, void *stream);
 
 /* ---- expert slot pool (LFU residency policy) and placement files ------------- */
 /* The reference's SlotPool (components/moe/include/ds41/store.hpp:80-157, store.cpp:15-196): a

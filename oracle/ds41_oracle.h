@@ -138,6 +138,19 @@ int oracle_moe_layer(const oracle_moe_config *cfg, const uint16_t *x, const floa
 int oracle_moe_layer_routed(const oracle_moe_config *cfg, const uint16_t *x, const int32_t *ids,
                             const float *w, const oracle_expert *experts, const oracle_expert *shared,
                             int m, uint16_t *y, int threads);
+/* components/dense/src/dense.cu:37-91 W8A8 (basic / parallel kernels): E4M3 weights w [n][k] with one
+ * E8M0 scale per 32 x 32 block ws [n/32][k/32], MXFP8 x [m][k] + xs [m][k/32]; per K32 group the exact
+ * dot (fp64, exact: products of two E4M3 values span < 2^49) rounded once to fp32, times sx then sw
+ * (fp32), added in ascending K into an fp32 accumulator; bf16 out. n % 32 == 0.
+ * Pinning: the shared per-group rule is pinned with the MXFP4 GEMM (Python brute force, one-hot and
+ * scale-linearity tests); the E4M3 weight decode and 32 x 32 block indexing by a Python brute force
+ * over random codes in tests/test_oracle_moe.py. */
+int oracle_dense_fp8(const uint8_t *w, const uint8_t *ws, const uint8_t *x, const uint8_t *xs, int m, int n,
+                     int k, float *acc_out, uint16_t *out_bf16);
+/* The FP8 shared expert (engine/src/hotpath/batch.inc:330-335 bshared): gate/up = dense_fp8 (bf16),
+ * components/dense/src/ops.cu:103-106 shared_act (SwiGLU limit 10, bf16, MXFP8), down = dense_fp8. */
+int oracle_shared_fp8_ffn(const oracle_expert *e, const uint8_t *xq, const uint8_t *xs, int m, int hidden,
+                          int inter, uint16_t *out_bf16);
 /* Worker threads used by oracle_mxfp4_gemm and oracle_expert_ffn (default 1). */
 void oracle_set_threads(int n);
 /* One routed/shared expert FFN on already-quantised input rows (the inner part of

@@ -133,6 +133,7 @@ typedef struct {
   int m, n, k;
   float *acc_out;
   uint16_t *out;
+  int fp8; /* 1: E4M3 weights [n][k], one E8M0 scale per 32 x 32 block [n/32][k/32] */
 } gemm_ctx;
 
 static void gemm_rows(void *p, int begin, int end) {
@@ -145,16 +146,23 @@ static void gemm_rows(void *p, int begin, int end) {
       int tn = c->m - t0 < 64 ? c->m - t0 : 64;
       for (int t = 0; t < tn; ++t) acc[t] = 0.0f;
       for (int g = 0; g < ng; ++g) {
-        const uint8_t *src = c->w + (size_t)row * (c->k / 2) + g * 16;
-        for (int i = 0; i < 16; ++i) {
-          wd[2 * i] = oracle_e2m1(src[i] & 15);
-          wd[2 * i + 1] = oracle_e2m1(src[i] >> 4);
+        float sw;
+        if (c->fp8) {
+          const uint8_t *src = c->w + (size_t)row * c->k + g * 32;
+          for (int i = 0; i < 32; ++i) wd[i] = oracle_e4m3(src[i]);
+          sw = oracle_e8m0(c->ws[(size_t)(row / 32) * ng + g]);
+        } else {
+          const uint8_t *src = c->w + (size_t)row * (c->k / 2) + g * 16;
+          for (int i = 0; i < 16; ++i) {
+            wd[2 * i] = oracle_e2m1(src[i] & 15);
+            wd[2 * i + 1] = oracle_e2m1(src[i] >> 4);
+          }
+          sw = oracle_e8m0(c->ws[(size_t)row * ng + g]);
         }
-        float sw = oracle_e8m0(c->ws[(size_t)row * ng + g]);
         for (int t = 0; t < tn; ++t) {
           const double *x = c->xd + (size_t)(t0 + t) * c->k + g * 32;
           double dot = 0.0;
-          for (int i = 0; i < 32; ++i) dot += x[i] * wd[i]; /* exact: < 2^33 span */
+          for (int i = 0; i < 32; ++i) dot += x[i] * wd[i]; /* exact: the products span < 2^49 */
           float cg = (float)dot;
           float term = (cg * c->sx[(size_t)(t0 + t) * ng + g]) * sw;
           acc[t] = acc[t] + term;
@@ -170,19 +178,23 @@ static void gemm_rows(void *p, int begin, int end) {
 }
 
 static int gemm_threads = 1;
-static int gemm_impl(const uint8_t *w, const uint8_t *ws, const uint8_t *x, const uint8_t *xs, int m,
-                     int n, int k, float *acc_out, uint16_t *out_bf16, int threads) {
-  if (m < 1 || n < 1 || k < 32 || k % 32) return -1;
+static int gemm_any(const uint8_t *w, const uint8_t *ws, const uint8_t *x, const uint8_t *xs, int m, int n,
+                    int k, float *acc_out, uint16_t *out_bf16, int threads, int fp8) {
+  if (m < 1 || n < 1 || k < 32 || k % 32 || (fp8 && n % 32)) return -1;
   double *xd = (double *)malloc(sizeof(double) * (size_t)m * k);
   float *sx = (float *)malloc(sizeof(float) * (size_t)m * (k / 32));
   if (!xd || !sx) { free(xd); free(sx); return -1; }
   for (size_t i = 0; i < (size_t)m * k; ++i) xd[i] = oracle_e4m3(x[i]);
   for (size_t i = 0; i < (size_t)m * (k / 32); ++i) sx[i] = oracle_e8m0(xs[i]);
-  gemm_ctx c = {w, ws, xd, sx, m, n, k, acc_out, out_bf16};
+  gemm_ctx c = {w, ws, xd, sx, m, n, k, acc_out, out_bf16, fp8};
   parallel_range(n, threads, gemm_rows, &c);
   free(xd);
   free(sx);
   return 0;
+}
+static int gemm_impl(const uint8_t *w, const uint8_t *ws, const uint8_t *x, const uint8_t *xs, int m,
+                     int n, int k, float *acc_out, uint16_t *out_bf16, int threads) {
+  return gemm_any(w, ws, x, xs, m, n, k, acc_out, out_bf16, threads, 0);
 }
 
 int oracle_mxfp4_gemm(const uint8_t *w, const uint8_t *ws, const uint8_t *x, const uint8_t *xs,
@@ -460,6 +472,31 @@ int oracle_moe_layer(const oracle_moe_config *cfg, const uint16_t *x, const floa
   rc = 0;
 done:
   free(logits); free(su); free(sb); free(ids); free(w);
+  return rc;
+}
+
+int oracle_dense_fp8(const uint8_t *w, const uint8_t *ws, const uint8_t *x, const uint8_t *xs, int m, int n,
+                     int k, float *acc_out, uint16_t *out_bf16) {
+  return gemm_any(w, ws, x, xs, m, n, k, acc_out, out_bf16, gemm_threads, 1);
+}
+
+int oracle_shared_fp8_ffn(const oracle_expert *e, const uint8_t *xq, const uint8_t *xs, int m, int hidden,
+                          int inter, uint16_t *out_bf16) {
+  int rc = -1;
+  uint16_t *g = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)m * inter);
+  uint16_t *u = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)m * inter);
+  uint16_t *h = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)m * inter);
+  uint8_t *hq = (uint8_t *)malloc((size_t)m * inter);
+  uint8_t *hs = (uint8_t *)malloc((size_t)m * inter / 32);
+  if (!g || !u || !h || !hq || !hs) goto done;
+  if (gemm_any(e->gate, e->gate_scale, xq, xs, m, inter, hidden, NULL, g, gemm_threads, 1)) goto done;
+  if (gemm_any(e->up, e->up_scale, xq, xs, m, inter, hidden, NULL, u, gemm_threads, 1)) goto done;
+  oracle_swiglu(g, u, NULL, h, m, inter, 10.0f);
+  if (oracle_quantize_mxfp8(h, hq, hs, m, inter)) goto done;
+  if (gemm_any(e->down, e->down_scale, hq, hs, m, hidden, inter, NULL, out_bf16, gemm_threads, 1)) goto done;
+  rc = 0;
+done:
+  free(g); free(u); free(h); free(hq); free(hs);
   return rc;
 }
 

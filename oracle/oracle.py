@@ -279,6 +279,30 @@ def expert_ffn(e, xq, xs, route_w, hidden, inter, limit=10.0):
     return out
 
 
+def dense_fp8(w, ws, xq, xs, m, n, k):
+    """W8A8 FP8 projection (32 x 32 block weight scales) -> (fp32 acc, bf16 bits) [m][n]."""
+    acc = np.empty((m, n), np.float32)
+    out = np.empty((m, n), np.uint16)
+    rc = lib().oracle_dense_fp8(_ptr(np.ascontiguousarray(w)), _ptr(np.ascontiguousarray(ws)),
+                                _ptr(np.ascontiguousarray(xq)), _ptr(np.ascontiguousarray(xs)), m, n, k, _ptr(acc),
+                                _ptr(out))
+    if rc:
+        raise ValueError("oracle_dense_fp8")
+    return acc, out
+
+
+def shared_fp8_ffn(e, xq, xs, hidden, inter):
+    """FP8 shared expert on quantised rows -> bf16 bits [m][hidden]."""
+    m = xq.shape[0]
+    out = np.empty((m, hidden), np.uint16)
+    es = _expert_struct(e)
+    rc = lib().oracle_shared_fp8_ffn(ctypes.byref(es), _ptr(np.ascontiguousarray(xq)), _ptr(np.ascontiguousarray(xs)),
+                                     m, hidden, inter, _ptr(out))
+    if rc:
+        raise ValueError("oracle_shared_fp8_ffn")
+    return out
+
+
 def moe_layer(x_bits, router_w, router_bias, experts, shared, hidden, inter, topk_=6, score_mode=0,
               route_scale=1.5, swiglu_limit=10.0, threads=0):
     """experts: list (len n_experts) of dicts of numpy arrays, or None for absent ones

@@ -258,3 +258,59 @@ def test_spark_topk3_tie_orders():
             assert len(set(ids[r].tolist())) == 3
             assert np.all(vals[:-1] >= vals[1:])
             assert sorted(vals.tolist()) == sorted(np.sort(s[r])[-3:].tolist())
+
+
+def rand_e4m3(rng, shape):
+    """Random E4M3 codes without the NaN codes 0x7f / 0xff."""
+    b = rng.integers(0, 256, shape, dtype=np.uint8)
+    b[(b & 0x7F) == 0x7F] = 0x3C
+    return b
+
+
+def python_dense_fp8(w, ws, x, xs, m, n, k):
+    """dense.cu:37-91 restated with Python floats: exact K32 dot of decoded E4M3 pairs, one fp32
+    rounding, times the activation then the 32x32-block weight scale in fp32, serial fp32 add."""
+    f = np.float32
+    ng = k // 32
+    out = np.zeros((m, n), np.float32)
+    for t in range(m):
+        for r in range(n):
+            acc = f(0)
+            for g in range(ng):
+                dot = sum(e4m3(int(x[t, 32 * g + i])) * e4m3(int(w[r, 32 * g + i])) for i in range(32))
+                sx = f(2.0 ** (int(xs[t, g]) - 127))
+                sw = f(2.0 ** (int(ws[r // 32, g]) - 127))
+                acc = f(acc + f(f(f(dot) * sx) * sw))
+            out[t, r] = acc
+    return out
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 32, 32), (3, 64, 96), (2, 96, 160)])
+def test_dense_fp8_vs_python(m, n, k):
+    rng = np.random.default_rng(m * 100 + n + k)
+    w = rand_e4m3(rng, (n, k))
+    ws = rng.integers(118, 130, (n // 32, k // 32), dtype=np.uint8)
+    x = rand_e4m3(rng, (m, k))
+    xs = rng.integers(118, 130, (m, k // 32), dtype=np.uint8)
+    acc, bits = O.dense_fp8(w, ws, x, xs, m, n, k)
+    want = python_dense_fp8(w, ws, x, xs, m, n, k)
+    assert np.array_equal(acc.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(bits, O.bf16_bits(want))
+
+
+def test_dense_fp8_one_hot_block_scales():
+    """One nonzero weight (row r, column c) and one nonzero activation at c: y[r] is their product
+    times 2^(sx-127) * 2^(sw-127) with sw the scale of block (r // 32, c // 32); other rows are 0."""
+    m, n, k = 1, 96, 128
+    for r, c in ((0, 0), (33, 70), (95, 127)):
+        w = np.zeros((n, k), np.uint8)
+        w[r, c] = 0x48  # 2^(9-7) * 1 = 4
+        x = np.zeros((m, k), np.uint8)
+        x[0, c] = 0xB4  # -(1 + 4/8) * 2^(6-7) = -0.75
+        ws = np.arange(n // 32 * (k // 32), dtype=np.uint8).reshape(n // 32, k // 32) + 120
+        xs = np.full((m, k // 32), 127, np.uint8)
+        xs[0, c // 32] = 129
+        acc, _ = O.dense_fp8(w, ws, x, xs, m, n, k)
+        want = 4.0 * -0.75 * 2.0 ** 2 * 2.0 ** (int(ws[r // 32, c // 32]) - 127)
+        assert acc[0, r] == np.float32(want)
+        assert np.count_nonzero(acc) == 1
