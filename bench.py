@@ -334,6 +334,66 @@ def zipf_route_ids(rng, perms, pool, T, K, s=1.1):
     return out
 
 
+def bench_fp8_shared(gpu, x_pool, wg, bias, table, steps, warmup, T=4, H=4096, I=2880, E=384, K=6, seed=5):
+    """configs[1] with the shared expert as the checkpoint stores it: FP8 E4M3 gate/up/down with one
+    E8M0 scale per 32 x 32 block (W8A8, MXFP8 activations), routed experts unchanged. Also the
+    standalone ds41_dense_fp8 at the shared expert's gate shape (M=4, N=2880, K=4096)."""
+    import ctypes
+    import torch
+    import ds41_gfx950 as G
+    g = torch.Generator(device=gpu).manual_seed(seed)
+
+    def fp8(n, k):  # N(0, 1) quantised per 32 x 32 block (amax -> 448), scaled to ~0.01
+        v = torch.randn((n, k), generator=g, device=gpu, dtype=torch.float32)
+        e = torch.ceil(torch.log2(v.abs().reshape(n // 32, 32, k // 32, 32).amax(dim=(1, 3)) / 448.0))
+        sc = torch.exp2(e).repeat_interleave(32, 0).repeat_interleave(32, 1)
+        w = (v / sc).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        return torch.where((w & 0x7F) == 0x7F, torch.full_like(w, 0x7E), w), (e + 121).to(torch.uint8)
+
+    gw_, gs_ = fp8(I, H)
+    uw_, us_ = fp8(I, H)
+    dw_, ds_ = fp8(H, I)
+    f8 = G.fp8_expert(dict(gate=gw_, gate_scale=gs_, up=uw_, up_scale=us_, down=dw_, down_scale=ds_))
+    pool = x_pool.shape[0]
+    y = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(G.layer_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
+    args = [G.make_layer_args(x_pool[i], wg, bias, table, 0, -1, T, H, I, E, K, y, ws) for i in range(pool)]
+    for a in args:
+        a.shared_fp8 = ctypes.addressof(f8)
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        G.moe_layer(args[i % pool], stream)
+    torch.cuda.synchronize()
+    ev = G.Events(2)
+    ev.record(0, stream)
+    for i in range(steps):
+        G.moe_layer(args[i % pool], stream)
+    ev.record(1, stream)
+    torch.cuda.synchronize()
+    layer_us = ev.elapsed(0, 1) * 1e3 / steps
+    xq, xs = G.dense_quant(x_pool[0])
+    yd = torch.empty((T, I), dtype=torch.bfloat16, device=gpu)
+    reps = max(steps, 50)
+    for _ in range(5):
+        G.lib().ds41_dense_fp8(G._p(xq), G._p(xs), G._p(gw_), G._p(gs_), G._p(yd), T, I, H, -1, G._stream(stream))
+    ev.record(0, stream)
+    for _ in range(reps):
+        G.lib().ds41_dense_fp8(G._p(xq), G._p(xs), G._p(gw_), G._p(gs_), G._p(yd), T, I, H, -1, G._stream(stream))
+    ev.record(1, stream)
+    torch.cuda.synchronize()
+    fp8_us = ev.elapsed(0, 1) * 1e3 / reps
+    if G.take_status():
+        raise AssertionError("fp8 shared bench: kernel status bits set")
+    wbytes = I * H + (I // 32) * (H // 32)
+    res = {"workload": "configs[1] layer with an FP8 W8A8 shared expert (32x32 block scales), routed MXFP4 unchanged",
+           "us_per_layer": layer_us, "tokens_per_s": T / (layer_us * 1e-6),
+           "shared_fp8_bytes": 3 * wbytes, "dense_fp8_us": fp8_us,
+           "dense_fp8_gbps": wbytes / (fp8_us * 1e-6) / 1e9, "dense_fp8_shape": [T, I, H]}
+    log(f"fp8 shared: layer {layer_us:.1f} us/step; ds41_dense_fp8 M={T} N={I} K={H}: {fp8_us:.1f} us, "
+        f"{res['dense_fp8_gbps']:.0f} GB/s")
+    return res
+
+
 def zipf_route_ids_fast(rng, perms, n, T, K, s=1.1):
     """As zipf_route_ids for n fresh step sets, vectorised: the top-K of log p + Gumbel noise is a
     sample of K distinct ranks drawn one after another with probability proportional to p."""
@@ -486,6 +546,7 @@ def main():
     ap.add_argument("--stack-warmup", type=int, default=20)
     ap.add_argument("--drafter-steps", type=int, default=300)
     ap.add_argument("--stack-cache-slots", type=int, default=1024)
+    ap.add_argument("--fp8-shared", type=int, default=1, help="0 skips the FP8 shared-expert leg")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -608,6 +669,9 @@ def main():
     log(f"gate_up_act {gate_gbps:.0f} GB/s, down {down_gbps:.0f} GB/s, layer {layer_gbps:.0f} GB/s "
         f"({layer_gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s), mean unique experts {mean_u:.2f}")
 
+    fp8_shared = bench_fp8_shared(gpu, x_pool, wg, bias, table, args.steps, args.warmup) \
+        if args.fp8_shared else None
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(x_pool_np[0], wg_np, bias_np, experts, H, I, E, args.cpu_seconds)
@@ -655,6 +719,7 @@ def main():
         "step40": stack,
         "prefill": prefill,
         "drafter_experts": drafter,
+        "fp8_shared": fp8_shared,
     }
     if stack and accept:  # acceptance time as a fraction of the 40-layer step (target < 3 %)
         out["accept"]["frac_of_step40"] = {m: accept["us_per_step"] * 1e-3 / r["ms_per_step"]

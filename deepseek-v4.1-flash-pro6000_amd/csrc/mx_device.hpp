@@ -11,6 +11,12 @@ namespace ds41g {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef const u32x4 __attribute__((address_space(1))) *global_u4;
+typedef const u32x2 __attribute__((address_space(1))) *global_u2;
+typedef u32x4 __attribute__((aligned(1))) u32x4_u;
+typedef const u32x4_u __attribute__((address_space(1))) *global_u4u;
 
 static_assert(sizeof(ds41_device_expert) == 64, "DeviceExpert must stay 64 bytes");
 static_assert(sizeof(ds41_gemm_job) == 32, "GemmJob must stay 32 bytes");
@@ -131,41 +137,74 @@ __device__ __forceinline__ v4f split_combine(v4f acc, int tokens) {
 // the E4M3 matrix x [*][k] and its scales xs [*][k/32]; with Split, the
 // split_rows(tokens) rows described above (padding rows zero, scale 127).
 // Returns the number of LDS rows. Caller syncs.
+// Each thread issues the global loads of up to four 16-byte pieces (or four
+// scale bytes) before it stores any of them, so a workgroup's staging costs
+// about one memory round trip instead of one per loop trip; with Split each
+// source piece is loaded once and stored as its two halves.
 template <bool Split = false, class RowIdx>
 __device__ __forceinline__ int stage_xtile(uint8_t *lq, uint8_t *ls, const uint8_t *x,
                                            const uint8_t *xs, int k, int tokens, RowIdx row_idx) {
   const int stride = xtile_stride(k), sstride = xtile_sstride(k);
   const int T4 = (tokens + 3) & ~3, nrows = Split ? 2 * T4 : tokens;
   const int pieces = (stride - 16) >> 4;  // includes the trailing zero chunk
-  const bool aligned = ((((uintptr_t)x) | (uintptr_t)k) & 15u) == 0;
-  for (int p = threadIdx.x; p < nrows * pieces; p += blockDim.x) {
-    const int r = p / pieces, off = (p - r * pieces) << 4;
-    const bool big = !Split || r < T4;
-    const int t = big ? r : r - T4;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (t < tokens && off < k) {
-      const uint8_t *src = x + (size_t)row_idx(t) * k + off;
-      if (aligned) v = *reinterpret_cast<const uint4 *>(src);
-      else {
-        uint8_t b[16];
-        for (int i = 0; i < 16; ++i) b[i] = src[i];
-        v = *reinterpret_cast<const uint4 *>(b);
-      }
-      if (Split) {
-        const uint32_t f = big ? 0u : 0xffffffffu;
-        v.x &= e4m3_big_mask(v.x) ^ f;
-        v.y &= e4m3_big_mask(v.y) ^ f;
-        v.z &= e4m3_big_mask(v.z) ^ f;
-        v.w &= e4m3_big_mask(v.w) ^ f;
+  const int kp = k >> 4;                  // pieces holding data (k % 32 == 0)
+  const bool aligned = (((uintptr_t)x) & 15u) == 0;
+  const int nsrc = tokens * kp;
+  for (int p0 = threadIdx.x; p0 < nsrc; p0 += 4 * blockDim.x) {
+    uint4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j * (int)blockDim.x;
+      v[j] = make_uint4(0, 0, 0, 0);
+      if (p < nsrc) {
+        const int t = p / kp, off = (p - t * kp) << 4;
+        const uint8_t *src = x + (size_t)row_idx(t) * k + off;
+        if (aligned) {
+          v[j] = *reinterpret_cast<const uint4 *>(src);
+        } else {
+          const u32x4 u = *(const u32x4_u *)(src);
+          v[j] = make_uint4(u.x, u.y, u.z, u.w);
+        }
       }
     }
-    *reinterpret_cast<uint4 *>(lq + r * stride + off) = v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j * (int)blockDim.x;
+      if (p >= nsrc) break;
+      const int t = p / kp, off = (p - t * kp) << 4;
+      if (Split) {
+        const uint4 m = make_uint4(e4m3_big_mask(v[j].x), e4m3_big_mask(v[j].y), e4m3_big_mask(v[j].z),
+                                   e4m3_big_mask(v[j].w));
+        *reinterpret_cast<uint4 *>(lq + t * stride + off) =
+            make_uint4(v[j].x & m.x, v[j].y & m.y, v[j].z & m.z, v[j].w & m.w);
+        *reinterpret_cast<uint4 *>(lq + (T4 + t) * stride + off) =
+            make_uint4(v[j].x & ~m.x, v[j].y & ~m.y, v[j].z & ~m.z, v[j].w & ~m.w);
+      } else {
+        *reinterpret_cast<uint4 *>(lq + t * stride + off) = v[j];
+      }
+    }
   }
-  const int ng = k >> 5;
-  for (int p = threadIdx.x; p < nrows * sstride; p += blockDim.x) {
-    const int r = p / sstride, g = p - r * sstride;
+  // zeros: the trailing chunk of every row and the whole of the padding rows
+  for (int p = threadIdx.x; p < nrows * pieces; p += blockDim.x) {
+    const int r = p / pieces, pc = p - r * pieces;
     const int t = (!Split || r < T4) ? r : r - T4;
-    ls[r * sstride + g] = g < ng && t < tokens ? xs[(size_t)row_idx(t) * ng + g] : (uint8_t)127;
+    if (pc >= kp || t >= tokens) *reinterpret_cast<uint4 *>(lq + r * stride + (pc << 4)) = make_uint4(0, 0, 0, 0);
+  }
+  const int ng = k >> 5, srows = Split ? T4 : tokens;
+  for (int p0 = threadIdx.x; p0 < srows * sstride; p0 += 4 * blockDim.x) {
+    uint8_t b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j * (int)blockDim.x, t = p / sstride, g = p - t * sstride;
+      b[j] = p < srows * sstride && g < ng && t < tokens ? xs[(size_t)row_idx(t) * ng + g] : (uint8_t)127;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j * (int)blockDim.x, t = p / sstride, g = p - t * sstride;
+      if (p >= srows * sstride) break;
+      ls[t * sstride + g] = b[j];
+      if (Split) ls[(T4 + t) * sstride + g] = b[j];
+    }
   }
   return nrows;
 }
@@ -208,12 +247,6 @@ __device__ __forceinline__ void split_chunk(const uint4 &lo, const uint4 &hi, v8
   }
 }
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef const u32x4 __attribute__((address_space(1))) *global_u4;
-typedef const u32x2 __attribute__((address_space(1))) *global_u2;
-typedef u32x4 __attribute__((aligned(1))) u32x4_u;
-typedef const u32x4_u __attribute__((address_space(1))) *global_u4u;
 
 // GScale: the weight scales come from global memory instead of an LDS row.
 // With each batch's weights a lane loads its channel's 32 scale bytes of that
@@ -327,13 +360,22 @@ struct Gemv16 {
 // q = l>>4, and the E8M0 of K32 block q. All 16 channels of a wave sit in one
 // 32-row scale block, so a lane's scales are bytes q, 4+q, 8+q, ... of that
 // block's scale row: one 16-byte load per batch of 4 chunks gives byte q of
-// dwords 0..3. Two batches of U = 4 chunks are in flight (ping-pong). Pieces at
-// k >= K (the partial last chunk) are zero; their activations are zero too.
+// its dwords. Pieces at k >= K (the partial last chunk) are zero; their
+// activations are zero too.
+//
+// A wave streams the chunk range [c0, c1) of its 16 weight rows in batches of
+// U = 4 chunks, two batches in flight (ping-pong), both issued by the
+// constructor. A serial-carry chain of
+// waves (f8_chain) splits K into contiguous ranges: every wave's loads are in
+// flight from the start, and the accumulator passes from wave to wave in K
+// order, so the sum is the same serial K-order sum one wave would form (the
+// reference's serial carry, dense.cu:38-91), with up to all of the tile's
+// weight bytes in flight at once.
 struct Gemv16F8 {
   static constexpr int U = 4;
   const uint8_t *w;   // weight row of this lane's channel
   const uint8_t *sr;  // scale row of the channel's 32-row block
-  int q, k, ng, nch, nb;
+  int q, k, ng, c0, c1, nb;
   uint4 A[U][2], B[U][2];
   uint4 SA, SB;
 
@@ -342,19 +384,21 @@ struct Gemv16F8 {
     const u32x4 v = *(global_u4u)(w + o);
     return off < k ? make_uint4(v.x, v.y, v.z, v.w) : make_uint4(0, 0, 0, 0);
   }
+  // first K32 group of the 16-group scale window loaded for batch b
+  __device__ __forceinline__ int window(int b) const {
+    const int g0 = 4 * (c0 + b * U);
+    return g0 + 16 <= ng ? g0 : (ng >= 16 ? ng - 16 : 0);
+  }
   __device__ __forceinline__ void load(uint4 (*buf)[2], uint4 &S, int b) const {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      int c = b * U + u;
-      c = c < nch ? c : nch - 1;
+      int c = c0 + b * U + u;
+      c = c < c1 ? c : (c1 > c0 ? c1 - 1 : 0);
       buf[u][0] = piece(128 * c + 16 * q);
       buf[u][1] = piece(128 * c + 64 + 16 * q);
     }
-    // scale dwords 4b .. 4b+3 (groups 16b .. 16b+15), clamped to the row
-    int g0 = 16 * b;
-    g0 = g0 + 16 <= ng ? g0 : (ng >= 16 ? ng - 16 : 0);
     if (ng >= 16) {
-      const u32x4 v = *(global_u4u)(sr + g0);
+      const u32x4 v = *(global_u4u)(sr + window(b));
       S = make_uint4(v.x, v.y, v.z, v.w);
     } else {  // short rows (k < 512): bytes clamped to the row, packed four to a dword
       uint32_t d[4] = {0u, 0u, 0u, 0u};
@@ -363,55 +407,53 @@ struct Gemv16F8 {
       S = make_uint4(d[0], d[1], d[2], d[3]);
     }
   }
-  __device__ __forceinline__ Gemv16F8(const uint8_t *wrow, const uint8_t *srow, int kk) {
+  __device__ __forceinline__ Gemv16F8(const uint8_t *wrow, const uint8_t *srow, int kk, int cbegin, int cend) {
     q = (threadIdx.x & 63) >> 4;
     w = wrow;
     sr = srow;
     k = kk;
     ng = kk >> 5;
-    nch = (ng + 3) >> 2;
-    nb = (nch + U - 1) / U;
-    load(A, SA, 0);
+    c0 = cbegin;
+    c1 = cend;
+    nb = (c1 - c0 + U - 1) / U;
+    load(A, SA, 0);  // both batches in flight before the wave's turn in a chain
+    if (nb > 1) load(B, SB, 1);
   }
-  // scale byte of K32 group 4c + q for chunk u of batch b (S loaded for batch b)
-  __device__ __forceinline__ int scale_of(const uint4 &S, int b, int u) const {
-    const int c = b * U + u, g = 4 * c + q;
-    const int gc = g < ng ? g : ng - 1;
-    int g0 = 16 * b;
-    g0 = g0 + 16 <= ng ? g0 : (ng >= 16 ? ng - 16 : 0);
-    const int idx = gc - g0;  // 0..15 within the loaded window
+  __device__ __forceinline__ int scale_of(const uint4 &S, int b, int c) const {
+    const int g = 4 * c + q, gc = g < ng ? g : ng - 1, idx = gc - window(b);
     const uint32_t d = (idx >> 2) == 0 ? S.x : (idx >> 2) == 1 ? S.y : (idx >> 2) == 2 ? S.z : S.w;
     return (int)((d >> (8 * (idx & 3))) & 0xffu);
   }
-  __device__ __forceinline__ v4f run(const XTile &xt) {
+  // Continues acc over the wave's chunk range.
+  __device__ __forceinline__ v4f run(const XTile &xt, v4f acc) {
     const int lane = threadIdx.x & 63, i = lane & 15;
     const int ii = i < xt.tokens ? i : 0;
     const uint8_t *xa = xt.q + ii * xt.stride + 16 * q;
     const uint8_t *sa = xt.s + ii * xt.sstride + q;
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
     auto compute = [&](const uint4 (*buf)[2], const uint4 &S, int b) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int c = b * U + u;
-        const int cx = c < nch ? c : nch;  // nch is the zero chunk
-        const uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * cx);
-        const uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * cx + 64);
+        const int c = c0 + b * U + u;
+        if (c >= c1) break;  // uniform: the rest belongs to the next wave of the chain
+        const uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * c);
+        const uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * c + 64);
         const v8i av = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
         const v8i bv = v8i{(int)buf[u][0].x, (int)buf[u][0].y, (int)buf[u][0].z, (int)buf[u][0].w,
                            (int)buf[u][1].x, (int)buf[u][1].y, (int)buf[u][1].z, (int)buf[u][1].w};
-        acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, 0, 0, 0, (int)sa[4 * cx], 0,
-                                                                scale_of(S, b, u));
+        acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, 0, 0, 0, (int)sa[4 * c], 0,
+                                                                scale_of(S, b, c));
       }
     };
+    if (nb <= 0) return acc;
+    // at entry A holds batch 0 and B batch 1; each buffer is refilled right after its compute
     int b = 0;
     for (; b + 2 < nb; b += 2) {
-      load(B, SB, b + 1);
       compute(A, SA, b);
       load(A, SA, b + 2);
       compute(B, SB, b + 1);
+      if (b + 3 < nb) load(B, SB, b + 3);
     }
     if (b + 2 == nb) {
-      load(B, SB, b + 1);
       compute(A, SA, b);
       compute(B, SB, b + 1);
     } else {
@@ -420,6 +462,32 @@ struct Gemv16F8 {
     return acc;
   }
 };
+
+// Chunk range of wave j of a Wc-wave chain over a k-long row.
+__device__ __forceinline__ void f8_chain_range(int k, int Wc, int j, int &c0, int &c1) {
+  const int nch = ((k >> 5) + 3) >> 2, per = (nch + Wc - 1) / Wc;
+  c0 = j * per < nch ? j * per : nch;
+  c1 = c0 + per < nch ? c0 + per : nch;
+}
+// Runs a Wc-wave serial-carry chain: in turn t, wave j == t continues the
+// accumulator the previous wave left in `carry` (LDS, 64 lanes x 4 floats of
+// this chain). Every wave of the workgroup calls it (the turns synchronise the
+// workgroup); the returned value is valid in the chain's last wave.
+template <int Wc>
+__device__ __forceinline__ v4f f8_chain(Gemv16F8 &g, const XTile &xt, float *carry, int j) {
+  const int lane = threadIdx.x & 63;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < Wc; ++t) {
+    if (j == t) {
+      if (t) acc = *reinterpret_cast<const v4f *>(carry + 4 * lane);
+      acc = g.run(xt, acc);
+      if (t + 1 < Wc) *reinterpret_cast<v4f *>(carry + 4 * lane) = acc;
+    }
+    __syncthreads();
+  }
+  return acc;
+}
 
 // Copy `bytes` contiguous bytes global -> LDS with the whole workgroup
 // (16-byte pieces when both ends allow it). Caller syncs.
