@@ -101,6 +101,7 @@ __device__ __forceinline__ const uint8_t *proj_scale(const ds41_device_expert &e
 struct XTile {
   const uint8_t *q, *s;
   int stride, sstride, tokens;
+  int split;  // 1: the GEMV feeds every row twice, as its |v| >= 1 and its |v| < 1 bytes
 };
 
 // One extra all-zero 128-k chunk (scales 127) follows the padded row, so a GEMV
@@ -123,8 +124,34 @@ __device__ __forceinline__ uint32_t e4m3_big_mask(uint32_t v) {
 // the window, and the two results are added in fp32. With T <= 8 tokens the
 // halves fill rows 0..T4-1 and T4..2*T4-1 (T4 = T rounded up to 4) of the
 // 16-row MFMA, so the split costs no extra MFMA: split_combine() adds each
-// token's two rows, which sit 4*T4 lanes apart.
+// token's two rows, which sit 4*T4 lanes apart. LDS holds each row once; a
+// lane masks its row's bytes to its half as it reads them (split_lane), so the
+// split costs no LDS either.
 __device__ __host__ __forceinline__ int split_rows(int tokens) { return 2 * ((tokens + 3) & ~3); }
+// MFMA row i (= lane & 15) of a split XTile: source row, and the mask flip
+// (0: |v| >= 1 bytes, ~0: |v| < 1 bytes) and keep (0 for rows past 2*T4).
+struct SplitLane {
+  int src;
+  uint32_t flip, keep;
+};
+__device__ __forceinline__ SplitLane split_lane(int i, int tokens, bool split) {
+  const int T4 = (tokens + 3) & ~3;
+  SplitLane r{i, 0u, 0xffffffffu};
+  if (split) {
+    r.src = i < T4 ? i : i - T4;
+    r.flip = i < T4 ? 0u : 0xffffffffu;
+    r.keep = i < 2 * T4 ? 0xffffffffu : 0u;
+  }
+  if (r.src >= tokens) r.src = 0;  // padding rows: any finite row, outputs dropped
+  return r;
+}
+__device__ __forceinline__ uint4 split_bytes(uint4 v, const SplitLane &l) {
+  v.x &= (e4m3_big_mask(v.x) ^ l.flip) & l.keep;
+  v.y &= (e4m3_big_mask(v.y) ^ l.flip) & l.keep;
+  v.z &= (e4m3_big_mask(v.z) ^ l.flip) & l.keep;
+  v.w &= (e4m3_big_mask(v.w) ^ l.flip) & l.keep;
+  return v;
+}
 __device__ __forceinline__ v4f split_combine(v4f acc, int tokens) {
   const int shift = 4 * ((tokens + 3) & ~3);
   v4f o;
@@ -134,18 +161,15 @@ __device__ __forceinline__ v4f split_combine(v4f acc, int tokens) {
 }
 
 // Stage `tokens` activation rows into LDS: LDS row r is source row row_idx(r) of
-// the E4M3 matrix x [*][k] and its scales xs [*][k/32]; with Split, the
-// split_rows(tokens) rows described above (padding rows zero, scale 127).
-// Returns the number of LDS rows. Caller syncs.
+// the E4M3 matrix x [*][k] and its scales xs [*][k/32], each row zero-padded
+// to its trailing zero chunk. Returns the number of rows. Caller syncs.
 // Each thread issues the global loads of up to four 16-byte pieces (or four
 // scale bytes) before it stores any of them, so a workgroup's staging costs
-// about one memory round trip instead of one per loop trip; with Split each
-// source piece is loaded once and stored as its two halves.
-template <bool Split = false, class RowIdx>
+// about one memory round trip instead of one per loop trip.
+template <class RowIdx>
 __device__ __forceinline__ int stage_xtile(uint8_t *lq, uint8_t *ls, const uint8_t *x,
                                            const uint8_t *xs, int k, int tokens, RowIdx row_idx) {
   const int stride = xtile_stride(k), sstride = xtile_sstride(k);
-  const int T4 = (tokens + 3) & ~3, nrows = Split ? 2 * T4 : tokens;
   const int pieces = (stride - 16) >> 4;  // includes the trailing zero chunk
   const int kp = k >> 4;                  // pieces holding data (k % 32 == 0)
   const bool aligned = (((uintptr_t)x) & 15u) == 0;
@@ -172,41 +196,96 @@ __device__ __forceinline__ int stage_xtile(uint8_t *lq, uint8_t *ls, const uint8
       const int p = p0 + j * (int)blockDim.x;
       if (p >= nsrc) break;
       const int t = p / kp, off = (p - t * kp) << 4;
-      if (Split) {
-        const uint4 m = make_uint4(e4m3_big_mask(v[j].x), e4m3_big_mask(v[j].y), e4m3_big_mask(v[j].z),
-                                   e4m3_big_mask(v[j].w));
-        *reinterpret_cast<uint4 *>(lq + t * stride + off) =
-            make_uint4(v[j].x & m.x, v[j].y & m.y, v[j].z & m.z, v[j].w & m.w);
-        *reinterpret_cast<uint4 *>(lq + (T4 + t) * stride + off) =
-            make_uint4(v[j].x & ~m.x, v[j].y & ~m.y, v[j].z & ~m.z, v[j].w & ~m.w);
-      } else {
-        *reinterpret_cast<uint4 *>(lq + t * stride + off) = v[j];
-      }
+      *reinterpret_cast<uint4 *>(lq + t * stride + off) = v[j];
     }
   }
-  // zeros: the trailing chunk of every row and the whole of the padding rows
-  for (int p = threadIdx.x; p < nrows * pieces; p += blockDim.x) {
-    const int r = p / pieces, pc = p - r * pieces;
-    const int t = (!Split || r < T4) ? r : r - T4;
-    if (pc >= kp || t >= tokens) *reinterpret_cast<uint4 *>(lq + r * stride + (pc << 4)) = make_uint4(0, 0, 0, 0);
+  for (int p = threadIdx.x; p < tokens * (pieces - kp); p += blockDim.x) {  // trailing zeros
+    const int r = p / (pieces - kp), pc = kp + (p - r * (pieces - kp));
+    *reinterpret_cast<uint4 *>(lq + r * stride + (pc << 4)) = make_uint4(0, 0, 0, 0);
   }
-  const int ng = k >> 5, srows = Split ? T4 : tokens;
-  for (int p0 = threadIdx.x; p0 < srows * sstride; p0 += 4 * blockDim.x) {
+  const int ng = k >> 5;
+  for (int p0 = threadIdx.x; p0 < tokens * sstride; p0 += 4 * blockDim.x) {
     uint8_t b[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int p = p0 + j * (int)blockDim.x, t = p / sstride, g = p - t * sstride;
-      b[j] = p < srows * sstride && g < ng && t < tokens ? xs[(size_t)row_idx(t) * ng + g] : (uint8_t)127;
+      b[j] = p < tokens * sstride && g < ng ? xs[(size_t)row_idx(t) * ng + g] : (uint8_t)127;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j * (int)blockDim.x;
+      if (p >= tokens * sstride) break;
+      ls[p] = b[j];
+    }
+  }
+  return tokens;
+}
+
+// Pre-split staging: split_rows(tokens) LDS rows, row t = the |v| >= 1 bytes of
+// source row t and row T4 + t its |v| < 1 bytes (padding rows zero, scales
+// 127), read by a GEMV with XTile.split = 0. It costs twice the LDS of
+// stage_xtile and saves the per-chunk masks of the read-time split; the
+// kernels take it where the doubled tile does not lower their occupancy.
+template <class RowIdx>
+__device__ __forceinline__ int stage_xtile_presplit(uint8_t *lq, uint8_t *ls, const uint8_t *x,
+                                                    const uint8_t *xs, int k, int tokens, RowIdx row_idx) {
+  const int stride = xtile_stride(k), sstride = xtile_sstride(k);
+  const int T4 = (tokens + 3) & ~3, nrows = 2 * T4;
+  const int pieces = (stride - 16) >> 4, kp = k >> 4;
+  const bool aligned = (((uintptr_t)x) & 15u) == 0;
+  const int nsrc = tokens * kp;
+  for (int p0 = threadIdx.x; p0 < nsrc; p0 += 4 * blockDim.x) {
+    uint4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j * (int)blockDim.x;
+      v[j] = make_uint4(0, 0, 0, 0);
+      if (p < nsrc) {
+        const int t = p / kp, off = (p - t * kp) << 4;
+        const uint8_t *src = x + (size_t)row_idx(t) * k + off;
+        if (aligned) {
+          v[j] = *reinterpret_cast<const uint4 *>(src);
+        } else {
+          const u32x4 u = *(const u32x4_u *)(src);
+          v[j] = make_uint4(u.x, u.y, u.z, u.w);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j * (int)blockDim.x;
+      if (p >= nsrc) break;
+      const int t = p / kp, off = (p - t * kp) << 4;
+      const SplitLane big{t, 0u, 0xffffffffu}, small{t, 0xffffffffu, 0xffffffffu};
+      *reinterpret_cast<uint4 *>(lq + t * stride + off) = split_bytes(v[j], big);
+      *reinterpret_cast<uint4 *>(lq + (T4 + t) * stride + off) = split_bytes(v[j], small);
+    }
+  }
+  for (int p = threadIdx.x; p < nrows * pieces; p += blockDim.x) {  // trailing chunk, padding rows
+    const int r = p / pieces, pc = p - r * pieces, t = r < T4 ? r : r - T4;
+    if (pc >= kp || t >= tokens) *reinterpret_cast<uint4 *>(lq + r * stride + (pc << 4)) = make_uint4(0, 0, 0, 0);
+  }
+  const int ng = k >> 5;
+  for (int p0 = threadIdx.x; p0 < T4 * sstride; p0 += 4 * blockDim.x) {
+    uint8_t b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
       const int p = p0 + j * (int)blockDim.x, t = p / sstride, g = p - t * sstride;
-      if (p >= srows * sstride) break;
-      ls[t * sstride + g] = b[j];
-      if (Split) ls[(T4 + t) * sstride + g] = b[j];
+      b[j] = p < T4 * sstride && g < ng && t < tokens ? xs[(size_t)row_idx(t) * ng + g] : (uint8_t)127;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j * (int)blockDim.x;
+      if (p >= T4 * sstride) break;
+      ls[p] = b[j];
+      ls[T4 * sstride + p] = b[j];
     }
   }
   return nrows;
+}
+// The pre-split tile when it fits `budget` bytes of LDS.
+__host__ __device__ __forceinline__ bool presplit_fits(int tokens, int k, int budget) {
+  return (size_t)split_rows(tokens) * (xtile_stride(k) + xtile_sstride(k)) <= (size_t)budget;
 }
 
 // Operand layout of V_MFMA_SCALE_F32_16X16X128_F8F6F4 (measured on gfx950):
@@ -301,16 +380,21 @@ struct Gemv16 {
   // xt: activation rows in LDS; lsw: this lane's weight-scale row in LDS (ng bytes).
   // Chunks past the end read the zero chunk of the activation rows (exact zero
   // products against a finite weight scale), so no MFMA sits behind a branch.
+  template <bool Split = false>
   __device__ __forceinline__ v4f run(const XTile &xt, const uint8_t *lsw) {
     const int lane = threadIdx.x & 63, q = lane >> 4, i = lane & 15;
-    const int ii = i < xt.tokens ? i : 0;  // padded rows repeat row 0; their outputs are dropped
-    const uint8_t *xa = xt.q + ii * xt.stride + 16 * q;
-    const uint8_t *sa = xt.s + ii * xt.sstride + q;
+    const SplitLane sl = split_lane(i, xt.tokens, Split);  // padded rows repeat row 0; outputs dropped
+    const uint8_t *xa = xt.q + sl.src * xt.stride + 16 * q;
+    const uint8_t *sa = xt.s + sl.src * xt.sstride + q;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     auto mma = [&](const uint4 &wv, int c, int sw) {
       const int cx = c < nch ? c : nch;  // nch is the zero chunk
-      const uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * cx);
-      const uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * cx + 64);
+      uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * cx);
+      uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * cx + 64);
+      if (Split) {
+        lo = split_bytes(lo, sl);
+        hi = split_bytes(hi, sl);
+      }
       const v8i bv = v8i{(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w, 0, 0, 0, 0};
       acc = mfma_chunk(lo, hi, bv, acc, (int)sa[4 * cx], sw);
     };
@@ -425,18 +509,23 @@ struct Gemv16F8 {
     return (int)((d >> (8 * (idx & 3))) & 0xffu);
   }
   // Continues acc over the wave's chunk range.
+  template <bool Split = false>
   __device__ __forceinline__ v4f run(const XTile &xt, v4f acc) {
     const int lane = threadIdx.x & 63, i = lane & 15;
-    const int ii = i < xt.tokens ? i : 0;
-    const uint8_t *xa = xt.q + ii * xt.stride + 16 * q;
-    const uint8_t *sa = xt.s + ii * xt.sstride + q;
+    const SplitLane sl = split_lane(i, xt.tokens, Split);
+    const uint8_t *xa = xt.q + sl.src * xt.stride + 16 * q;
+    const uint8_t *sa = xt.s + sl.src * xt.sstride + q;
     auto compute = [&](const uint4 (*buf)[2], const uint4 &S, int b) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c = c0 + b * U + u;
         if (c >= c1) break;  // uniform: the rest belongs to the next wave of the chain
-        const uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * c);
-        const uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * c + 64);
+        uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * c);
+        uint4 hi = *reinterpret_cast<const uint4 *>(xa + 128 * c + 64);
+        if (Split) {
+          lo = split_bytes(lo, sl);
+          hi = split_bytes(hi, sl);
+        }
         const v8i av = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
         const v8i bv = v8i{(int)buf[u][0].x, (int)buf[u][0].y, (int)buf[u][0].z, (int)buf[u][0].w,
                            (int)buf[u][1].x, (int)buf[u][1].y, (int)buf[u][1].z, (int)buf[u][1].w};
@@ -473,7 +562,7 @@ __device__ __forceinline__ void f8_chain_range(int k, int Wc, int j, int &c0, in
 // accumulator the previous wave left in `carry` (LDS, 64 lanes x 4 floats of
 // this chain). Every wave of the workgroup calls it (the turns synchronise the
 // workgroup); the returned value is valid in the chain's last wave.
-template <int Wc>
+template <int Wc, bool Split>
 __device__ __forceinline__ v4f f8_chain(Gemv16F8 &g, const XTile &xt, float *carry, int j) {
   const int lane = threadIdx.x & 63;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -481,7 +570,7 @@ __device__ __forceinline__ v4f f8_chain(Gemv16F8 &g, const XTile &xt, float *car
   for (int t = 0; t < Wc; ++t) {
     if (j == t) {
       if (t) acc = *reinterpret_cast<const v4f *>(carry + 4 * lane);
-      acc = g.run(xt, acc);
+      acc = g.template run<Split>(xt, acc);
       if (t + 1 < Wc) *reinterpret_cast<v4f *>(carry + 4 * lane) = acc;
     }
     __syncthreads();
