@@ -264,3 +264,35 @@ def test_prefill_matches_decode_layer_bitexact(gpu):
     dec = host(y_dec)
     say(f"  prefill vs decode: bit-identical {np.mean(got == dec):.5f}, tiles {tiles}")
     assert np.array_equal(got, dec)
+
+
+@pytest.mark.parametrize("H,I,E,T", [(4096, 2880, 64, 256), (576, 352, 16, 96)])
+def test_prefill_tiles_match_gemv_bitexact(gpu, H, I, E, T):
+    """Each token's output depends only on its own routes, and a tile row runs the decode GEMV's MFMA
+    sequence (chunks in ascending k, the magnitude halves into separate accumulators), so the layer
+    over all T tokens (experts with > 8 rows in 64-row tiles) must equal, bit for bit, the layer run
+    4 tokens at a time (every routed expert a GEMV job). H=576, I=352 cover partial K chunks and
+    slices, byte-wise scale loads and half-empty channel blocks."""
+    import ds41_gfx950 as G
+    K = 6
+    say(f"prefill tiles vs GEMV T={T} H={H} I={I} E={E}")
+    P, experts = make_experts(gpu, 80 + H, H, I, E)
+    rng = np.random.default_rng(81 + H)
+    x_np = rand_x(rng, T, H)
+    ids = zipf_ids(rng, T, E, K, perm=rng.permutation(E))
+    w = (rng.random((T, K)) + 0.1).astype(np.float32)
+    w = (w / w.sum(axis=1, keepdims=True) * 1.5).astype(np.float32)
+    G.take_status()
+    full, plan = run_prefill(gpu, experts, x_np, ids, w, H, I, E, K)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    assert plan == want_plan(counts, T) and plan[0] > (T + 63) // 64, plan
+    parts = []
+    for t0 in range(0, T, 4):
+        got, p4 = run_prefill(gpu, experts, x_np[t0:t0 + 4], ids[t0:t0 + 4], w[t0:t0 + 4], H, I, E, K)
+        assert p4[0] == 1  # only the shared expert's tile
+        parts.append(got)
+    chunked = np.concatenate(parts)
+    same = np.mean(full == chunked)
+    say(f"  plan {plan}, max rows {counts.max()}, bit-identical {same:.5f}")
+    assert np.array_equal(full, chunked)
+    assert G.take_status() == 0
