@@ -578,6 +578,16 @@ __device__ __forceinline__ v4f f8_chain(Gemv16F8 &g, const XTile &xt, float *car
   return acc;
 }
 
+// Workgroup barrier that orders LDS accesses only. __syncthreads() also
+// fences global memory, which makes every wave wait (s_waitcnt vmcnt(0)) for
+// all of its outstanding global loads, including prefetches meant to stay in
+// flight across the barrier; this fence waits for LDS operations only.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Copy `bytes` contiguous bytes global -> LDS with the whole workgroup
 // (16-byte pieces when both ends allow it). Caller syncs.
 __device__ __forceinline__ void stage_bytes(uint8_t *dst, const uint8_t *src, int bytes) {
