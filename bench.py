@@ -166,6 +166,27 @@ def bench_accept(gpu, steps, cpu_seconds, no_cpu, top_p=1.0):
 PEAK_FP4_TFLOPS = 10100.0
 
 
+def read_ceiling(gpu, stream, nbytes=1 << 30, blocks=2048, reps=10):
+    """GB/s of ds41_hbm_read_probe streaming nbytes once per launch (events around reps launches):
+    the practical read ceiling next to the published 8 TB/s."""
+    import torch
+    import ds41_gfx950 as G
+    buf = torch.ones(nbytes, dtype=torch.uint8, device=gpu)
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=gpu)
+    for _ in range(2):
+        G.hbm_read_probe(buf, sink, blocks, stream)
+    ev = G.Events(2)
+    torch.cuda.synchronize()
+    ev.record(0, stream)
+    for _ in range(reps):
+        G.hbm_read_probe(buf, sink, blocks, stream)
+    ev.record(1, stream)
+    torch.cuda.synchronize()
+    gbps = nbytes * reps / (ev.elapsed(0, 1) * 1e-3) / 1e9
+    del buf, sink
+    return gbps
+
+
 def bench_prefill(gpu, table, E, steps, warmup, seed=3):
     """one MoE layer chunked verify/prefill, T=512 rows bf16 N(0,1), each token routed to K=6
     distinct experts drawn from Zipf(1.1) over ranks (rank r -> expert perm[r-1], seeded permutation), route
@@ -670,6 +691,10 @@ def main():
     log(f"gate_up_act {gate_gbps:.0f} GB/s, down {down_gbps:.0f} GB/s, layer {layer_gbps:.0f} GB/s "
         f"({layer_gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s), mean unique experts {mean_u:.2f}")
 
+    ceiling = read_ceiling(gpu, stream)
+    log(f"streaming-read ceiling (ds41_hbm_read_probe, 1 GiB, 2048 WGs): {ceiling:.0f} GB/s; "
+        f"gate_up_act at {gate_gbps / ceiling * 100:.1f}% of it")
+
     fp8_shared = bench_fp8_shared(gpu, x_pool, wg, bias, table, args.steps, args.warmup) \
         if args.fp8_shared else None
 
@@ -713,7 +738,8 @@ def main():
         "launch_us": launch_us,
         "roofline": {"bound": "hbm", "kernel": "layer_gate_up_act_kernel", "achieved": gate_gbps,
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": gate_gbps / PEAK_HBM_GBPS, "traffic": GATE_UP_TRAFFIC_BYTES,
-                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, calibrated)"},
+                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, calibrated)",
+                     "measured_read_ceiling": ceiling, "frac_of_measured_ceiling": gate_gbps / ceiling},
         "cpu_baseline": cpu,
         "accept": accept,
         "accept_top_p": accept_tp,

@@ -10,3 +10,4 @@
 #include "expert_records.inc"
 #include "accept.inc"
 #include "spark_gpu.inc"
+#include "read_probe.inc"

@@ -260,6 +260,14 @@ def router_weights(u, ids, scale=1.5, stream=None):
 
 
 # ---- fused layer ------------------------------------------------------------------
+def hbm_read_probe(buf, sink, blocks, stream=None):
+    """Streams buf (a uint8 CUDA tensor, 16-byte multiple) once with `blocks` workgroups; sink
+    holds blocks * 256 uint32 words. Time it to get the device's streaming-read ceiling."""
+    f = lib().ds41_hbm_read_probe
+    f.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    check(f(buf.data_ptr(), buf.numel(), sink.data_ptr(), blocks, _stream(stream)), "ds41_hbm_read_probe")
+
+
 def layer_workspace_bytes(T, H, I, E, K):
     return lib().ds41_moe_layer_workspace_bytes(T, H, I, E, K)
 

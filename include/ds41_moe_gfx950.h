@@ -477,6 +477,13 @@ int ds41_event_record(void *event, void *stream);
 
 /* Library version string. */
 const char *ds41_gfx950_version(void);
+
+/* Measurement utility with no counterpart in the reference: streams `bytes`
+ * (a multiple of 16, 16-byte aligned) from device memory with `blocks`
+ * workgroups of 256 threads and writes one word per thread to `sink`
+ * (device, blocks * 256 * 4 bytes). Timing it gives the practical HBM read
+ * ceiling that the HBM-bound kernels' rates are compared against. */
+int ds41_hbm_read_probe(const void *buf, size_t bytes, void *sink, int blocks, void *stream);
 /* Reads and clears the kernels' status bits (synchronous): 1 a residency wait
  * gave up, 2 a job's row count was outside 1..8, 4 invalid/duplicate routes. */
 int ds41_take_status(uint32_t *status);

@@ -90,3 +90,14 @@ def test_target_experts_abi_host_checks():
     assert lib.ds41_target_experts(None, 0, None, None, None, None, 1, None) == -1
     assert lib.ds41_target_experts_destroy(None) == 1
     assert lib.ds41_spark_topk3_gpu(None, None, 1, None) == 1
+
+
+def test_read_probe_host_checks():
+    """ds41_hbm_read_probe rejects bad sizes and pointers before any launch (no GPU needed)."""
+    lib = ctypes.CDLL(LIB)
+    f = lib.ds41_hbm_read_probe
+    f.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    assert f(None, 1024, ctypes.c_void_p(256), 4, None) != 0
+    assert f(ctypes.c_void_p(256), 1000, ctypes.c_void_p(256), 4, None) != 0   # not a multiple of 16
+    assert f(ctypes.c_void_p(264), 1024, ctypes.c_void_p(256), 4, None) != 0   # misaligned
+    assert f(ctypes.c_void_p(256), 1024, ctypes.c_void_p(256), 0, None) != 0   # no workgroups
