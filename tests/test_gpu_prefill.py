@@ -170,8 +170,10 @@ def check_tokens(experts, x_np, ids, w, got, H, I, E, tokens):
 
 
 @pytest.mark.parametrize("T,E,skew", [(300, 32, "uniform"), (256, 32, "zipf"), (77, 64, "zipf"), (1, 8, "uniform"),
-                                      (40, 32, "uniform")])
+                                      (40, 32, "uniform"), (300, 1024, "zipf")])
 def test_prefill_layer_vs_oracle(gpu, T, E, skew):
+    """(300, 1024) takes the plan's key-sort path (5 groups x 1024 experts of token bitmaps exceed
+    its LDS); the others its counting path."""
     import ds41_gfx950 as G
     H, I, K = 512, 256, 6
     say(f"prefill layer T={T} H={H} I={I} E={E} routing={skew}")
