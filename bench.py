@@ -1,6 +1,6 @@
 """Benchmark of the ds41 speculative-verify MoE path on one MI355X.
 
-Default workload: one MoE layer decode verify with
+Default workload (configs[1] of the benchmark definition): one MoE layer decode verify with
 T=4 rows (1 committed + 3 MTP drafts), hidden 4096, 384 routed experts
 (intermediate 2880, MXFP4 e2m1 + e8m0/32) top-6 + 1 shared expert, all
 resident in HBM; router fp32 N(0, 0.02^2), inputs bf16 N(0, 1). A step is one

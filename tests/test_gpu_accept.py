@@ -1,6 +1,6 @@
 """GPU acceptance sampler vs the reference's host sampler, through the C ABI.
 
-Bar (BASELINE north_star): accept/reject decisions and resampled token ids are
+Bar: accept/reject decisions and resampled token ids are
 bit-exact given identical fp32 logits and Philox uniforms. The golden results
 come from the reference's own compiled sampler (tests/golden/accept_v2.json);
 the sequential exact path (flags bit 0) must give the same answers."""

@@ -3,7 +3,7 @@ ops.cu:103-106, batch.inc:330-335) against the oracle, through the C ABI.
 
 Bars: MXFP8 quantisation and the shared-expert activation bit-exact; projections, the shared
 expert and the MoE layer with an FP8 shared expert within rel-L2 1e-3 of the oracle's exact
-per-block result (the BASELINE north_star bar for MoE outputs)."""
+per-block result (the bar for MoE outputs)."""
 import sys
 
 import numpy as np

@@ -1,6 +1,6 @@
 """GPU parity of the gfx950 MoE kernels against the oracle, through the C ABI.
 
-Bars (BASELINE north_star): MXFP4 dequant and MXFP8 quant bit-exact; router
+Bars: MXFP4 dequant and MXFP8 quant bit-exact; router
 top-k indices, route weights and the ordered reduction bit-exact given
 identical inputs; projections and the MoE layer within rel-L2 1e-3 of the
 oracle's fp32-accumulate result."""

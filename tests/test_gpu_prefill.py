@@ -3,7 +3,7 @@ the component GEMM (ds41_mxfp4_prefill_raw, ds41_grouped_mxfp4_prefill) and the
 prefill MoE layer (ds41_moe_prefill_layer: device route plan, fused gate/up +
 SwiGLU + MXFP8, down, ordered reduce) against the oracle.
 
-Bar (BASELINE north_star): MoE outputs within rel-L2 1e-3 of the oracle's fp32
+Bar: MoE outputs within rel-L2 1e-3 of the oracle's fp32
 accumulation; routing is the caller's, so the plan itself must be exact (every
 token's rows summed in ascending expert id, shared expert last)."""
 import sys

@@ -2,7 +2,7 @@
 ds41_spark_sample_gpu_v2, engine/third_party/spark/src/sampling.cu:6-49) on the
 GPU against the oracle's restatement of the reference kernel, through the C ABI.
 
-Bar (BASELINE north_star): accept/reject decisions and token ids bit-exact.
+Bar: accept/reject decisions and token ids bit-exact.
 The measures are random fp32 rows whose fp64 sums round, so the kernel's
 summation orders (strided mass + tree, chunked draw prefix) are exercised; the
 oracle itself is pinned to the compiled reference host sampler on exact sums

@@ -5,7 +5,7 @@ The host tier changes where a routed expert's bytes come from (a staging slot
 filled by hipMemcpyAsync instead of its HBM slab), never the arithmetic: the
 same step with every expert resident must give bit-identical outputs, ids and
 weights. Each layer's output is also checked against the oracle's MoE layer
-(rel-L2 1e-3, BASELINE north_star) given the layer's input and routing."""
+(rel-L2 1e-3) given the layer's input and routing."""
 import sys
 
 import numpy as np
