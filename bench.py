@@ -665,9 +665,10 @@ def main():
         G.moe_layer(a, stream)
     reps = max(args.steps // pool, 1)
     launch_us = {}
-    for j, n in ((2, "gate_up_act"), (3, "down")):
+    # "down" is the fused down + reduce kernel; the separate pair (stage bit 5) is timed beside it
+    for mask, n in ((4, "gate_up_act"), (8, "down"), (8 | 32, "down_separate"), (16 | 32, "reduce_separate")):
         for a in prep:
-            a.stage_mask = 1 << j
+            a.stage_mask = mask
         G.moe_layer(prep[-1], stream)
         torch.cuda.synchronize()
         ev.record(0, stream)
@@ -687,7 +688,9 @@ def main():
     layer_gbps = layer_bytes / (total_ms * 1e-3) / 1e9
     log("stage avg us (start/stop timestamps, include dispatch): " +
         ", ".join(f"{n} {avg[n] * 1e3:.1f}" for n in names))
-    log(f"launch avg us (back to back): gate_up_act {launch_us['gate_up_act']:.1f}, down {launch_us['down']:.1f}")
+    log(f"launch avg us (back to back): gate_up_act {launch_us['gate_up_act']:.1f}, down+reduce (fused) "
+        f"{launch_us['down']:.1f}; separate kernels: down {launch_us['down_separate']:.1f}, "
+        f"reduce {launch_us['reduce_separate']:.1f}")
     log(f"gate_up_act {gate_gbps:.0f} GB/s, down {down_gbps:.0f} GB/s, layer {layer_gbps:.0f} GB/s "
         f"({layer_gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s), mean unique experts {mean_u:.2f}")
 
