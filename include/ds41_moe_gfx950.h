@@ -146,9 +146,11 @@ typedef struct ds41_moe_layer_args {
                                      reduce) in order (hipExtLaunchKernel) */
   uint32_t stage_mask;            /* 0: every kernel. Otherwise bit i launches kernel i only (for
                                      timing one kernel on a workspace a full call has prepared).
-                                     When 512 <= inter <= 4096, kernel 3 is the fused down projection
-                                     and reduction and kernel 4 launches nothing (its two events
-                                     mark an empty interval). Bit 5 keeps the separate down and
+                                     When the activation rows of all jobs fit the fused kernel's
+                                     150 KB LDS tile ((tokens*topk + tokens) rows of about inter
+                                     bytes: tokens <= 6 at topk 6, inter 2880), kernel 3 is the
+                                     fused down projection and reduction and kernel 4 launches
+                                     nothing (its two events mark an empty interval). Bit 5 keeps the separate down and
                                      reduce kernels (same output bits); alone it means every kernel. */
   const ds41_device_expert *shared_fp8; /* optional host struct: the shared expert as the checkpoint
                                      stores it, FP8 E4M3 gate/up [inter][hidden] and down
