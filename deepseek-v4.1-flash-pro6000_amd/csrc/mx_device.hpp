@@ -75,14 +75,22 @@ __device__ __forceinline__ uint32_t mxfp8_exponent(float amax) {
   return (b >> 23) + ((b & 0x7fffffu) != 0u);
 }
 
-// Bounded acquire-wait on a residency flag (mxfp4.cu:36-43 semantics). Returns
-// false after ~2 s without the expected generation, so no wave can spin forever.
+// Bounded acquire-wait on a residency flag (mxfp4.cu:36-43 semantics): relaxed
+// device-coherent polls, then one acquire fence once the expected generation is
+// seen. Gives up after kReadyWaitTicks of the 100 MHz constant wall clock
+// (2 s), so no wave can spin forever.
+constexpr uint64_t kReadyWaitTicks = 200000000ull;
 __device__ __forceinline__ bool wait_ready(const ds41_device_expert &e) {
   if (!e.ready) return true;
-  for (uint32_t i = 0; i < (1u << 25); ++i) {
-    uint32_t v = __hip_atomic_load(e.ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-    if (v == e.generation) return true;
-    __builtin_amdgcn_s_sleep(2);
+  const uint64_t t0 = wall_clock64();
+  for (;;) {
+    const uint32_t v = __hip_atomic_load(e.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v == e.generation) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      return true;
+    }
+    if (wall_clock64() - t0 > kReadyWaitTicks) break;
+    __builtin_amdgcn_s_sleep(8);
   }
   atomicOr(&ds41_status, kStatusReadyTimeout);
   return false;

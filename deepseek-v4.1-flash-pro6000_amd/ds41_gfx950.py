@@ -331,6 +331,7 @@ def moe_layer(args, stream=None):
     check(lib().ds41_moe_verify_layer(ctypes.byref(args), _stream(stream)), "moe_verify_layer")
 
 
+
 class Events:
     """n hipEvents owned by the library (timing on a given stream)."""
 

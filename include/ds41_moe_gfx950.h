@@ -24,7 +24,9 @@ extern "C" {
  * (components/moe/include/ds41/store.hpp:110-117 DeviceExpert, 64 B;
  *  components/moe/include/ds41/kernels.cuh:8-13 GemmJob, 32 B).
  * ready == NULL: ordering is the caller's (stream/event); otherwise kernels
- * wait until *ready == generation (acquire) before reading the weights. */
+ * wait until *ready == generation (acquire) before reading the weights. The
+ * wait is bounded (about 2 s); when it gives up, status bit 1 is set and the
+ * outputs that needed the expert are written as NaN (ds41_take_status). */
 typedef struct ds41_device_expert {
   const uint8_t *gate, *gate_scale;
   const uint8_t *up, *up_scale;
@@ -36,7 +38,7 @@ typedef struct ds41_device_expert {
 
 typedef struct ds41_gemm_job {
   uint32_t expert;          /* index into the DeviceExpert table */
-  int32_t tokens;           /* 1..16 rows for this expert */
+  int32_t tokens;           /* 1..8 rows for this expert (the prefill entry takes up to max_tokens) */
   const uint8_t *x;         /* E4M3 [tokens][k] */
   const uint8_t *x_scale;   /* E8M0 [tokens][k/32] */
   void *output;             /* BF16 [tokens][n] */
@@ -491,7 +493,8 @@ const char *ds41_gfx950_version(void);
  * ceiling that the HBM-bound kernels' rates are compared against. */
 int ds41_hbm_read_probe(const void *buf, size_t bytes, void *sink, int blocks, void *stream);
 /* Reads and clears the kernels' status bits (synchronous): 1 a residency wait
- * gave up, 2 a job's row count was outside 1..8, 4 invalid/duplicate routes. */
+ * gave up (the rows that needed those weights are written as NaN), 2 a job's
+ * row count was outside 1..8, 4 invalid/duplicate routes. */
 int ds41_take_status(uint32_t *status);
 
 #ifdef __cplusplus

@@ -1,0 +1,154 @@
+"""The DeviceExpert residency flags (components/moe/include/ds41/store.hpp:110-117 `ready` /
+`generation`; the kernels' acquire wait, components/moe/src/mxfp4.cu:36-43), through the C ABI.
+
+Bars:
+- flags that already hold each expert's generation give output bits identical to ready == NULL,
+  for the verify layer (gate/up, fused down + reduce) and the grouped projection API;
+- flags written by a copy on another stream after the layer is queued: the kernels wait for them,
+  the status word stays 0 and the output bits are again identical;
+- a flag that the host never sets (the bounded wait's failure path, forced from the host): status
+  bit 1 is raised, every output that needed the expert is NaN and the others are unchanged. The
+  wait gives up after 2 s of the device's wall clock, so every kernel still exits."""
+import time
+
+import numpy as np
+import pytest
+
+from test_gpu_moe import dev, host, make_layer, rand_mx, rand_x, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _flagged(experts, flags, gen):
+    """Copies of the expert dicts whose table entries carry ready = &flags[i], generation gen[i]."""
+    out = []
+    for i, e in enumerate(experts):
+        d = dict(e)
+        d["ready"] = flags.data_ptr() + 4 * i
+        d["generation"] = int(gen[i])
+        out.append(d)
+    return out
+
+
+def _layer_inputs(gpu, T, H, E, seed):
+    rng = np.random.default_rng(seed)
+    x = dev(rand_x(rng, T, H), gpu)
+    wg = dev((rng.standard_normal((E, H)) * 0.02).astype(np.float32), gpu)
+    bias = dev(np.zeros(E, np.float32), gpu)
+    return x, wg, bias
+
+
+def _run_layer(gpu, table, x, wg, bias, T, H, I, E, K, stream=None):
+    import torch
+    import ds41_gfx950 as G
+    y = torch.full((T, H), float("nan"), dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(G.layer_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
+    ids = torch.full((T, K), -1, dtype=torch.int32, device=gpu)
+    a = G.make_layer_args(x, wg, bias, table, 0, E, T, H, I, E, K, y, ws, ids_out=ids)
+    if stream is not None:  # the fills above run on the current stream
+        stream.wait_stream(torch.cuda.current_stream())
+    G.moe_layer(a, stream=stream)
+    return y, ids, ws
+
+
+def test_ready_flags_already_set_match_no_flags(gpu):
+    import torch
+    import ds41_gfx950 as G
+    T, H, I, E, K = 4, 4096, 2880, 64, 6
+    say(f"ready flags already set: layer T={T} H={H} I={I} E={E}")
+    P, experts = make_layer(gpu, 51, H, I, E, T)
+    gen = np.arange(E + 1, dtype=np.uint32) * 7 + 3
+    flags = torch.from_numpy(gen.astype(np.int32)).to(gpu)
+    plain, _ = G.device_table(experts, gpu)
+    flagged, _ = G.device_table(_flagged(experts, flags, gen), gpu)
+    x, wg, bias = _layer_inputs(gpu, T, H, E, 52)
+    y0, i0, _ = _run_layer(gpu, plain, x, wg, bias, T, H, I, E, K)
+    y1, i1, _ = _run_layer(gpu, flagged, x, wg, bias, T, H, I, E, K)
+    torch.cuda.synchronize()
+    assert G.take_status() == 0
+    assert np.array_equal(host(i0), host(i1))
+    assert np.array_equal(host(y0), host(y1))
+    assert not np.any((host(y1) & 0x7fff) > 0x7f80)
+    # the grouped projection API reads the same flags
+    rng = np.random.default_rng(53)
+    n, k, m = 512, 1024, 3
+    w, ws = rand_mx(rng, n, k)
+    e = {"gate": dev(w, gpu), "gate_scale": dev(ws, gpu)}
+    xq, xs = G.quantize_mxfp8(dev(rand_x(rng, m, k), gpu))
+    outs = []
+    for ready in (False, True):
+        ee = dict(e)
+        if ready:
+            ee.update(ready=flags.data_ptr() + 8, generation=int(gen[2]))
+        table, _ = G.device_table([ee], gpu)
+        out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+        jobs = G.device_jobs([(0, m, xq, xs, out)], gpu)
+        G.grouped(table, jobs, 1, G.PROJ_GATE, n, k)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert G.take_status() == 0
+    assert np.array_equal(host(outs[0]), host(outs[1]))
+
+
+def test_ready_flags_written_by_another_stream(gpu):
+    """The layer is queued first; the flags arrive from pinned host memory on a second stream."""
+    import torch
+    import ds41_gfx950 as G
+    T, H, I, E, K = 4, 2048, 1024, 48, 6
+    say(f"ready flags from another stream: layer T={T} H={H} I={I} E={E}")
+    P, experts = make_layer(gpu, 54, H, I, E, T)
+    gen = (np.arange(E + 1, dtype=np.uint32) + 1) * 5
+    flags = torch.zeros(E + 1, dtype=torch.int32, device=gpu)
+    plain, _ = G.device_table(experts, gpu)
+    flagged, _ = G.device_table(_flagged(experts, flags, gen), gpu)
+    x, wg, bias = _layer_inputs(gpu, T, H, E, 55)
+    y0, _, _ = _run_layer(gpu, plain, x, wg, bias, T, H, I, E, K)
+    torch.cuda.synchronize()
+    src = torch.from_numpy(gen.astype(np.int32)).pin_memory()
+    compute, copy = torch.cuda.Stream(), torch.cuda.Stream()  # default priority, non-blocking
+    t0 = time.time()
+    y1, _, ws = _run_layer(gpu, flagged, x, wg, bias, T, H, I, E, K, stream=compute)
+    with torch.cuda.stream(copy):
+        flags.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    dt = time.time() - t0
+    say(f"  layer with flags set after queueing finished in {dt * 1e3:.1f} ms")
+    assert G.take_status() == 0
+    assert np.array_equal(host(y0), host(y1))
+
+
+def test_ready_flag_never_set_gives_nan_and_status(gpu):
+    """A flag the host never sets on the shared expert (forced failure of the bounded wait): the
+    wait gives up, status bit 1, and every token's output is NaN (the shared expert feeds every
+    token). Then the grouped API: only the job whose expert never became ready is NaN."""
+    import torch
+    import ds41_gfx950 as G
+    T, H, I, E, K = 2, 512, 256, 16, 2
+    say(f"ready flag never set (bounded wait gives up after 2 s): layer T={T} H={H} I={I} E={E}")
+    P, experts = make_layer(gpu, 56, H, I, E, T)
+    flags = torch.zeros(E + 1, dtype=torch.int32, device=gpu)
+    ex = [dict(e) for e in experts]
+    ex[E]["ready"], ex[E]["generation"] = flags.data_ptr() + 4 * E, 1  # never written
+    table, _ = G.device_table(ex, gpu)
+    x, wg, bias = _layer_inputs(gpu, T, H, E, 57)
+    t0 = time.time()
+    y, _, _ = _run_layer(gpu, table, x, wg, bias, T, H, I, E, K)
+    torch.cuda.synchronize()
+    say(f"  layer returned after {time.time() - t0:.2f} s")
+    assert G.take_status() & 1
+    assert np.all((host(y) & 0x7fff) > 0x7f80), "every output must be NaN"
+    rng = np.random.default_rng(58)
+    n, k, m = 128, 512, 2
+    w, s = rand_mx(rng, n, k)
+    good = {"gate": dev(w, gpu), "gate_scale": dev(s, gpu)}
+    bad = dict(good, ready=flags.data_ptr(), generation=9)
+    table, _ = G.device_table([good, bad], gpu)
+    xq, xs = G.quantize_mxfp8(dev(rand_x(rng, m, k), gpu))
+    o_good = torch.zeros((m, n), dtype=torch.bfloat16, device=gpu)
+    o_bad = torch.zeros((m, n), dtype=torch.bfloat16, device=gpu)
+    jobs = G.device_jobs([(0, m, xq, xs, o_good), (1, m, xq, xs, o_bad)], gpu)
+    G.grouped(table, jobs, 2, G.PROJ_GATE, n, k)
+    torch.cuda.synchronize()
+    assert G.take_status() & 1
+    assert np.all((host(o_bad) & 0x7fff) > 0x7f80)
+    assert not np.any((host(o_good) & 0x7fff) > 0x7f80)
