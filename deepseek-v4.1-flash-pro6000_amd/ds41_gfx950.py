@@ -97,6 +97,7 @@ def lib():
             raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
         _lib = ctypes.CDLL(LIB_PATH)
         _lib.ds41_moe_layer_workspace_bytes.restype = ctypes.c_size_t
+        _lib.ds41_moe_layer_noalloc_max_bytes.restype = ctypes.c_size_t
         _lib.ds41_moe_prefill_workspace_bytes.restype = ctypes.c_size_t
         _lib.ds41_gfx950_version.restype = ctypes.c_char_p
         _lib.ds41_spark_accept_workspace_bytes.restype = ctypes.c_size_t
@@ -330,6 +331,15 @@ def dense_shared_act(g, u, stream=None):
 def moe_layer(args, stream=None):
     check(lib().ds41_moe_verify_layer(ctypes.byref(args), _stream(stream)), "moe_verify_layer")
 
+
+def moe_layer_noalloc_rc(args, stream=None):
+    """ds41_moe_verify_layer_noalloc: the layer on the library's fixed device workspace (the
+    args' workspace fields are ignored). Returns the HIP error code."""
+    return lib().ds41_moe_verify_layer_noalloc(ctypes.byref(args), _stream(stream))
+
+
+def moe_layer_noalloc_max_bytes():
+    return lib().ds41_moe_layer_noalloc_max_bytes()
 
 
 class Events:

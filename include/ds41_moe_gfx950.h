@@ -165,6 +165,17 @@ size_t ds41_moe_layer_workspace_bytes(int tokens, int hidden, int inter, int n_e
                                       int topk);
 
 int ds41_moe_verify_layer(const ds41_moe_layer_args *args, void *stream);
+/* No counterpart in the reference. For callers that cannot allocate (code under
+ * HIP graph capture, serving loops that forbid hipMalloc): ds41_moe_verify_layer
+ * with its workspace in a fixed device array of ds41_moe_layer_noalloc_max_bytes()
+ * (1.5 MiB) that each GPU holds until the process ends. args->workspace and
+ * workspace_bytes are ignored; shapes whose workspace
+ * (ds41_moe_layer_workspace_bytes) exceeds the array return hipErrorInvalidValue.
+ * It calls no allocator. Every call on one GPU shares that GPU's array and leaves
+ * the last call's plan in it (a stage_mask call reads it); calls that overlap
+ * on one GPU (different streams without ordering) race. */
+int ds41_moe_verify_layer_noalloc(const ds41_moe_layer_args *args, void *stream);
+size_t ds41_moe_layer_noalloc_max_bytes(void);
 /* Reads the route plan of the last layer call from its workspace (host copy, synchronous):
  * unique expert count and ids; returns the count or -1. */
 int ds41_moe_layer_plan(const void *workspace, int tokens, int hidden, int inter, int n_experts,
