@@ -76,7 +76,7 @@ class StackDesc(ctypes.Structure):
 class StackStats(ctypes.Structure):
     _fields_ = [("steps", ctypes.c_uint64), ("layers", ctypes.c_uint64), ("resident_routed", ctypes.c_uint64),
                 ("host_fetched", ctypes.c_uint64), ("h2d_bytes", ctypes.c_uint64),
-                ("invalid_layers", ctypes.c_uint64)]
+                ("invalid_layers", ctypes.c_uint64), ("cached_routed", ctypes.c_uint64)]
 
 
 assert ctypes.sizeof(DeviceExpert) == 64 and ctypes.sizeof(GemmJob) == 32
@@ -473,7 +473,8 @@ class HostSlabs:
 
 class CacheStats(ctypes.Structure):
     _fields_ = [("requests", ctypes.c_uint64), ("hits", ctypes.c_uint64), ("misses", ctypes.c_uint64),
-                ("evictions", ctypes.c_uint64), ("h2d_bytes", ctypes.c_uint64)]
+                ("evictions", ctypes.c_uint64), ("h2d_bytes", ctypes.c_uint64), ("slots", ctypes.c_uint64),
+                ("prefetch_requests", ctypes.c_uint64), ("prefetch_copies", ctypes.c_uint64)]
 
 
 class VerifyStack:
@@ -510,9 +511,29 @@ class VerifyStack:
                                             _p(weights_out), _stream(stream)), "ds41_verify_stack_layer")
 
     def cache(self, slots, placement=None):
-        """ds41_verify_stack_cache: an HBM cache of `slots` expert slabs for the host-tier experts."""
+        """ds41_verify_stack_cache: an HBM cache of `slots` expert slabs for the host-tier experts
+        (slots <= 0: as many as the free HBM holds, less 2 GiB)."""
         check(lib().ds41_verify_stack_cache(self.handle, slots, None if placement is None else ctypes.byref(placement)),
               "ds41_verify_stack_cache")
+
+    def prefetch_rc(self, layers, experts):
+        """ds41_verify_stack_prefetch over (layer, expert) pairs; returns the HIP error code."""
+        import numpy as np
+        la = np.ascontiguousarray(np.asarray(layers, np.int32).ravel())
+        ea = np.ascontiguousarray(np.asarray(experts, np.int32).ravel())
+        return lib().ds41_verify_stack_prefetch(self.handle, la.ctypes.data_as(ctypes.c_void_p),
+                                                ea.ctypes.data_as(ctypes.c_void_p), len(la))
+
+    def prefetch(self, layers, experts):
+        check(self.prefetch_rc(layers, experts), "ds41_verify_stack_prefetch")
+
+    def prefetch_routes(self, route_ids):
+        """Prefetches every (layer, expert) pair of a host int32 [L][T][K] route array."""
+        import numpy as np
+        r = np.asarray(route_ids, np.int32)
+        L = r.shape[0]
+        layers = np.repeat(np.arange(L, dtype=np.int32), r[0].size)
+        self.prefetch(layers, r.reshape(-1))
 
     def cache_stats(self):
         st = CacheStats()

@@ -274,10 +274,11 @@ typedef struct ds41_stack_desc {
 /* Cumulative counters of the layers that have a host tier (read back each layer). */
 typedef struct ds41_stack_stats {
   uint64_t steps, layers;          /* layers = layer passes with a host tier */
-  uint64_t resident_routed;        /* routed experts served from HBM (shared excluded) */
-  uint64_t host_fetched;           /* host-tier experts copied in */
+  uint64_t resident_routed;        /* routed experts served from their table's HBM slabs (shared excluded) */
+  uint64_t host_fetched;           /* host-tier experts copied in (on demand or by a prefetch) */
   uint64_t h2d_bytes;
   uint64_t invalid_layers;         /* layer passes whose routes were rejected */
+  uint64_t cached_routed;          /* routed host-tier experts the HBM cache already held at the plan */
 } ds41_stack_stats;
 
 /* Creates a stack (allocates: the layer workspace, max_tokens*topk staging
@@ -387,9 +388,11 @@ int ds41_pool_reset_history(void *pool);
 
 /* Dynamic HBM cache for the stack's host-tier experts, the reference's VRAM slot pool in front
  * of its host tier (components/moe/src/offload.cpp:240-381 load, SlotPool policy store.cpp).
- * Allocates `slots` expert slabs in HBM (slots >= max_tokens * topk), a pinned patch buffer and
- * one event per layer; call before the first step or between steps. A routed host-tier expert
- * that the pool holds is read in place (a hit); a miss is copied from its host slab into the
+ * Allocates `slots` expert slabs in HBM (slots <= 0: as many as the free HBM holds less a 2 GiB
+ * reserve, at most layers * n_experts; at least max_tokens * topk), a device map of the cached
+ * experts, a pinned patch buffer and events; call before the first step or between steps
+ * (synchronous; an existing cache is dropped). A routed host-tier expert that the pool holds is
+ * read in place with the resident experts (a hit); a miss is copied from its host slab into the
  * slot the policy assigns, after the copy stream has waited for the last layer that read the
  * slot's previous expert. `policy` (nullable: recent 6, decay 32, distinct, soft, no budgets)
  * applies its recent/decay/lfu/pools/budget fields to the stack's layers (policy->layers must
@@ -398,10 +401,23 @@ int ds41_pool_reset_history(void *pool);
 int ds41_verify_stack_cache(void *stack, int slots, const ds41_placement *policy);
 typedef struct ds41_cache_stats {
   uint64_t requests;                 /* routed host-tier experts served through the cache */
-  uint64_t hits, misses, evictions;
-  uint64_t h2d_bytes;
+  uint64_t hits, misses, evictions;  /* hits include experts a prefetch brought in */
+  uint64_t h2d_bytes;                /* demand and prefetch copies */
+  uint64_t slots;                    /* the cache's size in expert slabs */
+  uint64_t prefetch_requests;        /* host-tier experts named by prefetches */
+  uint64_t prefetch_copies;          /* of which copied in (the others were cached) */
 } ds41_cache_stats;
 int ds41_verify_stack_cache_stats(void *stack, ds41_cache_stats *out);
+/* Prefetch into the HBM cache (the reference's prefetch_experts, engine/src/hotpath/streamed.inc:
+ * 89-108, components/moe/src/offload.cpp): host arrays of n (layer, expert) pairs that the caller
+ * expects the coming layers to route. Host-tier experts the cache lacks are acquired (one pool
+ * call; the LFU history is left alone), copied in on the copy stream and leased until their layer
+ * is next processed; HBM-resident experts are skipped. The layer's plan then finds them in the
+ * cache: the step waits (on the device) for a layer's prefetch copies before that layer's plan,
+ * and no host-tier copy stands between its plan and its down projection. Call between layers or
+ * steps, never while another thread uses the stack. Requires a cache. More experts than the
+ * unleased slots: hipErrorOutOfMemory and nothing changes. */
+int ds41_verify_stack_prefetch(void *stack, const int32_t *layers, const int32_t *experts, int n);
 
 /* ---- on-disk expert format: records manifest over safetensors shards ------------- */
 /* load_records (components/moe/src/manifest.cpp:35-55): the manifest written by the reference's

@@ -53,7 +53,7 @@ def test_stack_abi_host_checks():
     import sys
     sys.path.insert(0, os.path.join(ROOT, "deepseek-v4.1-flash-pro6000_amd"))
     import ds41_gfx950 as G
-    assert ctypes.sizeof(G.StackLayer) == 56 and ctypes.sizeof(G.StackStats) == 48
+    assert ctypes.sizeof(G.StackLayer) == 56 and ctypes.sizeof(G.StackStats) == 56
     off, slab = G.slab_layout(4096, 2880)
     # the reference's offload slot: 18,800,640 B per expert (gate/up/down weights + e8m0 scales)
     assert slab == 18800640 and off == [0, 5898240, 6266880, 12165120, 12533760, 18432000]

@@ -219,10 +219,12 @@ def test_stack_layer_entry_matches_step(gpu):
         assert np.array_equal(host(cur).view(np.uint8), (y if l == L - 1 else lo[l]).view(np.uint8))
 
 
-def host_demands(ids, host_sets, E):
-    """Per layer, the host-tier experts the plan hands to the cache: distinct routed ids in the host
-    set, ascending (the plan numbers jobs by expert id), as flattened ids l * E + e."""
-    return [[l * E + e for e in sorted(set(ids[l].ravel().tolist()) & host_sets[l])] for l in range(len(host_sets))]
+def host_demand(ids_l, host_set, l, E, model):
+    """The host-tier experts of layer l in the order the stack hands them to its pool: the ones the
+    cache already holds (the plan's HBM jobs), then the others, each ascending by expert id, as
+    flattened ids l * E + e. `model` is a pool in the stack pool's state."""
+    want = [l * E + e for e in sorted(set(ids_l.ravel().tolist()) & host_set)]
+    return [f for f in want if model.residency(f) >= 0] + [f for f in want if model.residency(f) < 0]
 
 
 @pytest.mark.parametrize("slots,budget", [(24, None), (40, (10, 18, 12))])
@@ -262,7 +264,8 @@ def test_stack_cache_bitexact_and_policy(gpu, slots, budget):
         a = st.run("tier", x, route)
         b = st.run("all", x, route)
         check_same(a, b)
-        for want in host_demands(rid, st.host_sets, E):
+        for l in range(L):
+            want = host_demand(rid[l], st.host_sets[l], l, E, model)
             if not want:
                 continue
             rc, got = model.acquire(want)
@@ -277,3 +280,86 @@ def test_stack_cache_bitexact_and_policy(gpu, slots, budget):
     assert cs["hits"] == hits and cs["misses"] == misses and cs["evictions"] == evictions
     assert cs["requests"] == hits + misses and cs["h2d_bytes"] == misses * st.slab
     assert hits > 0 and evictions > 0
+    ss = st.tier.stats()
+    assert ss["cached_routed"] == hits  # every hit was found in the map by the plan (no prefetch here)
+
+
+def random_routes(rng, st, L, T, K, E, step):
+    rid = np.empty((L, T, K), np.int32)
+    for l in range(L):
+        hs = sorted(st.host_sets[l])
+        for t in range(T):  # mostly host-tier experts, some resident ones
+            pool = hs[:10] if step % 2 else hs
+            n_host = int(rng.integers(3, 6))
+            pick = list(rng.choice(pool, n_host, replace=False))
+            rest = [e for e in range(E) if e not in st.host_sets[l]]
+            pick += list(rng.choice(rest, K - n_host, replace=False))
+            rid[l, t] = pick
+    return rid
+
+
+def test_stack_cache_prefetch_bitexact(gpu):
+    """Prefetch (ds41_verify_stack_prefetch) of each step's routes into a small HBM cache before the
+    step: every output equals the all-resident stack's bit for bit, every routed host-tier expert is
+    found in the cache by its layer's plan (no demand miss), and the prefetch copies and evictions
+    equal the library's slot pool replaying the same prefetch-then-demand sequence."""
+    import torch
+    import ds41_gfx950 as G
+    L, H, I, E, K, T, slots = 3, 512, 256, 32, 6, 4, 40
+    say(f"stack cache + prefetch slots={slots} L={L} E={E} T={T}")
+    st = Stack(gpu, 33, L, H, I, E, K, T, [range(l, E, 2) for l in range(L)])
+    st.tier.cache(slots)
+    model = G.ExpertPool(slots, [E] * L)
+    rng = np.random.default_rng(34)
+    copies = evictions = demand = 0
+    G.take_status()
+    c0, s0 = st.tier.cache_stats(), st.tier.stats()
+    for step in range(10):
+        rid = random_routes(rng, st, L, T, K, E, step)
+        st.tier.prefetch_routes(rid)
+        want = []  # the prefetch batch: per layer in order, first-seen host-tier ids
+        for l in range(L):
+            for e in rid[l].ravel().tolist():
+                f = l * E + e
+                if e in st.host_sets[l] and f not in want:
+                    want.append(f)
+        rc, pref = model.acquire(want, prefetch=True)
+        assert rc == len(want)
+        copies += sum(not g[2] for g in pref)
+        evictions += sum(g[3] >= 0 for g in pref)
+        route = torch.from_numpy(rid).to(gpu)
+        x = rand_x(gpu, 60 + step, T, H)
+        a = st.run("tier", x, route)
+        b = st.run("all", x, route)
+        check_same(a, b)
+        for l in range(L):
+            dem = host_demand(rid[l], st.host_sets[l], l, E, model)
+            if dem:
+                rc, got = model.acquire(dem)
+                assert rc == len(dem) and all(g[2] for g in got)
+                demand += len(dem)
+                assert model.release(got) == 0
+            assert model.release([g for g in pref if g[0] // E == l]) == 0
+    assert G.take_status() == 0
+    c1, s1 = st.tier.cache_stats(), st.tier.stats()
+    d = {k: c1[k] - c0[k] for k in c1 if k != "slots"}
+    say(f"  cache {d}")
+    assert d["misses"] == 0 and d["hits"] == demand and d["requests"] == demand
+    assert d["prefetch_copies"] == copies and d["evictions"] == evictions and evictions > 0
+    assert d["h2d_bytes"] == copies * st.slab
+    assert s1["cached_routed"] - s0["cached_routed"] == demand
+
+
+def test_stack_prefetch_rejects_bad_pairs(gpu):
+    L, H, I, E, K, T = 2, 512, 256, 32, 6, 4
+    st = Stack(gpu, 35, L, H, I, E, K, T, [range(0, 8), range(8, 16)])
+    assert st.tier.prefetch_rc([0], [1]) == 1  # no cache yet
+    st.tier.cache(24)
+    assert st.tier.prefetch_rc([2], [1]) == 1 and st.tier.prefetch_rc([0], [E]) == 1
+    assert st.tier.prefetch_rc([0, 1], [20, 3]) == 0  # both HBM-resident: nothing to fetch
+    many = list(range(0, 8)) + list(range(8, 16)) + list(range(0, 8))
+    assert st.tier.prefetch_rc([0] * 8 + [1] * 8, many[:16]) == 0
+    cs = st.tier.cache_stats()
+    assert cs["prefetch_requests"] == 16 and cs["prefetch_copies"] == 16
+    x = rand_x(gpu, 70, T, H)
+    check_same(st.run("tier", x), st.run("all", x))  # leases end as the layers run
