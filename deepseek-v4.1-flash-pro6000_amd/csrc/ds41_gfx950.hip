@@ -9,5 +9,6 @@
 #include "verify_stack.inc"
 #include "expert_records.inc"
 #include "accept.inc"
+#include "spark_host.inc"
 #include "spark_gpu.inc"
 #include "read_probe.inc"

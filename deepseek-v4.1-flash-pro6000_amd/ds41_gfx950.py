@@ -101,6 +101,14 @@ def lib():
         _lib.ds41_moe_prefill_workspace_bytes.restype = ctypes.c_size_t
         _lib.ds41_gfx950_version.restype = ctypes.c_char_p
         _lib.ds41_spark_accept_workspace_bytes.restype = ctypes.c_size_t
+        _lib.ds41_spark_sample_workspace_bytes.restype = ctypes.c_size_t
+        _lib.ds41_spark_sample_logits_gpu_v2.argtypes = [
+            ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_uint64,
+            ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+            ctypes.c_int, ctypes.c_void_p]
+        _lib.ds41_spark_error.restype = ctypes.c_char_p
+        _lib.ds41_spark_rng_word_v2.restype = ctypes.c_uint32
+        _lib.ds41_spark_uniform_v2.restype = ctypes.c_double
         _lib.ds41_spark_verify_gpu_v2.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                                   ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64,
                                                   ctypes.c_void_p, ctypes.c_void_p]
@@ -384,6 +392,78 @@ def verify_logits(target, draft, drafts_dev, temperature, top_p, seed, step, out
         target.data_ptr(), 0 if draft is None else draft.data_ptr(), 0 if k == 0 else drafts_dev.data_ptr(), k, V,
         float(temperature), float(top_p), seed, step, out.data_ptr(), workspace.data_ptr(), workspace.numel(),
         flags, _stream(stream).value), "ds41_spark_verify_logits_gpu_v2")
+
+
+def sample_workspace(rows, vocab, device="cuda"):
+    import torch
+    return torch.zeros(lib().ds41_spark_sample_workspace_bytes(rows, vocab), dtype=torch.uint8, device=device)
+
+
+def sample_logits_rc(logits, temperature, top_p, seed, step, first_slot, purpose, tokens, workspace, flags=0,
+                     stream=None):
+    """ds41_spark_sample_logits_gpu_v2 over logits [rows][V] fp32 -> tokens int32 [rows]; returns the rc."""
+    rows, V = logits.shape
+    return lib().ds41_spark_sample_logits_gpu_v2(
+        logits.data_ptr(), rows, V, float(temperature), float(top_p), seed, step, first_slot, purpose,
+        tokens.data_ptr(), workspace.data_ptr(), workspace.numel(), flags, _stream(stream).value)
+
+
+def sample_logits(logits, temperature, top_p, seed, step, first_slot, purpose, tokens, workspace, flags=0,
+                  stream=None):
+    check(sample_logits_rc(logits, temperature, top_p, seed, step, first_slot, purpose, tokens, workspace, flags,
+                           stream), "ds41_spark_sample_logits_gpu_v2")
+
+
+# ---- host sampler C ABI (spark.h) -----------------------------------------------------
+def spark_error():
+    return lib().ds41_spark_error().decode()
+
+
+def spark_probabilities(x, temperature, top_p):
+    """Host fp64 probability row of fp32 logits x (numpy), or None on error."""
+    import numpy as np
+    x = np.ascontiguousarray(x, np.float32)
+    p = np.empty(x.shape[0], np.float64)
+    rc = lib().ds41_spark_probabilities(x.ctypes.data_as(ctypes.c_void_p), p.ctypes.data_as(ctypes.c_void_p),
+                                        x.shape[0], ctypes.c_double(temperature), ctypes.c_double(top_p))
+    return p if rc == 0 else None
+
+
+def spark_sample_v2(p, seed, step, slot, purpose):
+    """Host draw from the fp64 row p; None on error."""
+    import numpy as np
+    p = np.ascontiguousarray(p, np.float64)
+    tok = ctypes.c_int32(-1)
+    rc = lib().ds41_spark_sample_v2(p.ctypes.data_as(ctypes.c_void_p), p.shape[0], ctypes.c_uint64(seed),
+                                    ctypes.c_uint64(step), ctypes.c_uint32(slot), ctypes.c_uint32(purpose),
+                                    ctypes.byref(tok))
+    return tok.value if rc == 0 else None
+
+
+def spark_verify_v2(d, q, p, greedy, seed, step):
+    """Host verify_v2 over fp64 rows; a result tuple, or None on error."""
+    import numpy as np
+    k, V = p.shape[0] - 1, p.shape[1]
+    p = np.ascontiguousarray(p, np.float64)
+    q = None if q is None else np.ascontiguousarray(q, np.float64)
+    d = np.ascontiguousarray(np.asarray(d, np.int32)) if k else None
+    res = SparkResult()
+    vp = lambda a: ctypes.c_void_p(0) if a is None else a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    rc = lib().ds41_spark_verify_v2(vp(d), vp(q), vp(p), k, V, greedy, ctypes.c_uint64(seed), ctypes.c_uint64(step),
+                                    ctypes.byref(res))
+    if rc:
+        return None
+    return (tuple(res.tokens[:res.emitted]), res.accepted_drafts, res.accepted_input_rows, res.rejected)
+
+
+def spark_rng_word_v2(seed, step, slot, purpose, draw):
+    return lib().ds41_spark_rng_word_v2(ctypes.c_uint64(seed), ctypes.c_uint64(step), ctypes.c_uint32(slot),
+                                        ctypes.c_uint32(purpose), ctypes.c_uint64(draw))
+
+
+def spark_uniform_v2(seed, step, slot, purpose, draw):
+    return lib().ds41_spark_uniform_v2(ctypes.c_uint64(seed), ctypes.c_uint64(step), ctypes.c_uint32(slot),
+                                       ctypes.c_uint32(purpose), ctypes.c_uint64(draw))
 
 
 def result_tuple(buf):

@@ -57,6 +57,49 @@ int ds41_spark_sample_gpu_v2(const float *p, int vocab, uint64_t seed, uint64_t 
  * zeroed (synchronous read). */
 int ds41_spark_accept_fallbacks(const void *workspace, int drafts, int vocab, uint32_t *count);
 
+/* Philox v2 purposes (spark.h:109). */
+enum ds41_spark_purpose { DS41_SPARK_TARGET = 0, DS41_SPARK_DRAFT = 1, DS41_SPARK_ACCEPT = 2, DS41_SPARK_RESIDUAL = 3 };
+
+/* Token sampling from fp32 logits on the device: for each row r of logits [rows][vocab], the
+ * engine's sample(probabilities(x_r, T, top_p), rng, step, first_slot + r, purpose)
+ * (engine/src/sampling.cpp:205-226), which SpeculativeStep uses to draw draft token k from q_k
+ * with (step, k, DS41_SPARK_DRAFT) (engine/src/speculation.cpp:147-155); T == 0 gives the first
+ * argmax (speculation.cpp:149). tokens: device int32 [rows], -1 for a row with a non-finite
+ * logit. Tokens equal the host sampler's: a draw whose margin is within the bound on the
+ * difference between parallel and sequential fp64 sums is redone with sequential sums.
+ * rows 1..6 with first_slot + rows - 1 <= 5, purpose 0..3; flags bit 0 forces the sequential
+ * path (testing). Workspace: ds41_spark_sample_workspace_bytes(rows, vocab) device bytes; calls
+ * sharing one workspace must be ordered. No counterpart entry in the reference (its drafts are
+ * sampled on the host). */
+size_t ds41_spark_sample_workspace_bytes(int rows, int vocab);
+int ds41_spark_sample_logits_gpu_v2(const float *logits, int rows, int vocab, double temperature,
+                                    double top_p, uint64_t seed, uint64_t step, uint32_t first_slot,
+                                    uint32_t purpose, int32_t *tokens, void *workspace,
+                                    size_t workspace_bytes, int flags, void *stream);
+
+/* ---- host sampler C ABI (engine/third_party/spark/include/ds41/spark.h:115-132), host memory.
+ * Each returns 0 (or the value) on success and -1 (a word: 0, a uniform: NaN) on invalid input,
+ * with the reason in ds41_spark_error(), a thread-local string valid until the thread's next
+ * failing call. The results equal libds41_spark's bit for bit. */
+const char *ds41_spark_error(void);
+/* p [vocab] = exp((x - x_b) / t) / z in fp64 (b = first argmax, z summed in index order), T == 0
+ * one-hot at b; top_p < 1 keeps the shortest prefix in (p desc, index asc) order whose
+ * sequential mass reaches top_p and divides by that mass. */
+int ds41_spark_probabilities(const float *logits, double *p, int vocab, double temperature,
+                             double top_p);
+uint32_t ds41_spark_rng_word_v2(uint64_t seed, uint64_t step, uint32_t slot, uint32_t purpose,
+                                uint64_t draw);
+double ds41_spark_uniform_v2(uint64_t seed, uint64_t step, uint32_t slot, uint32_t purpose,
+                             uint64_t draw);
+/* One token of the normalised row p with uniform 0 of (seed, step, slot, purpose). */
+int ds41_spark_sample_v2(const double *p, int vocab, uint64_t seed, uint64_t step, uint32_t slot,
+                         uint32_t purpose, int32_t *token);
+/* The accept/reject/residual/bonus decisions over p [(drafts+1)][vocab] and q [drafts][vocab]
+ * (q may be NULL when greedy), drafts <= 5. */
+int ds41_spark_verify_v2(const int32_t *drafts_ids, const double *q, const double *p, int drafts,
+                         int vocab, int greedy, uint64_t seed, uint64_t step,
+                         ds41_spark_result *out);
+
 #ifdef __cplusplus
 }
 #endif

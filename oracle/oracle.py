@@ -82,6 +82,38 @@ def ref():
     return _ref
 
 
+REFENGINE_PATH = os.path.join(HERE, "_ref", "libds41_refengine.so")
+_refengine = None
+
+
+def refengine():
+    """The reference engine's accept sampler (engine/src/sampling.cpp with its 8-thread
+    probabilities_rows) behind oracle/refengine_shim.cpp, compiled from the reference sources by
+    `make -C oracle ref`. None when it was not built."""
+    global _refengine
+    if _refengine is None and os.path.exists(REFENGINE_PATH):
+        R = ctypes.CDLL(REFENGINE_PATH)
+        R.refeng_accept_step.argtypes = [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_double,
+                                         ctypes.c_uint64, ctypes.c_uint64, P, P]
+        R.refeng_probabilities.argtypes = [P, ctypes.c_int, ctypes.c_double, ctypes.c_double, P]
+        _refengine = R
+    return _refengine
+
+
+def ref_accept_step(target, draft, drafts, temperature, top_p, seed, step):
+    """refeng_accept_step: (draft tokens, ds41_spark_result as a tuple), or None when it throws."""
+    R = refengine()
+    V = target.shape[1]
+    d = np.full(max(drafts, 1), -1, np.int32)
+    res = SparkResult()
+    rc = R.refeng_accept_step(_ptr(np.ascontiguousarray(target, np.float32)),
+                              _ptr(None if draft is None else np.ascontiguousarray(draft, np.float32)), drafts, V,
+                              temperature, top_p, seed, step, _ptr(d), ctypes.byref(res))
+    if rc:
+        return None
+    return d[:drafts].tolist(), res.as_tuple()
+
+
 REFPOOL_PATH = os.path.join(HERE, "_ref", "libds41_refpool.so")
 _refpool = None
 
