@@ -25,6 +25,7 @@
 #include <filesystem>
 #include <fstream>
 #include <iomanip>
+#include <iterator>
 #include <map>
 #include <memory>
 #include <sstream>
@@ -272,28 +273,46 @@ class JsonReader {
   }
 };
 
-// ---- the safetensors checkpoint ------------------------------------------------
-struct CkptTensor {
-  std::string name, path, dtype;
-  std::vector<uint64_t> shape;
-  uint64_t offset = 0, bytes = 0, file_bytes = 0;
+// ---- byte ranges ---------------------------------------------------------------
+struct Range {
+  uint64_t lo = 0, len = 0;
 };
-
-inline uint64_t add_checked(uint64_t a, uint64_t b) {
-  if (a > UINT64_MAX - b) throw RecordError("tensor offset overflow");
-  return a + b;
+// inner lies within outer (an empty inner may sit at outer's end).
+inline bool range_within(const Range &outer, const Range &inner) {
+  if (inner.lo < outer.lo) return false;
+  const uint64_t rel = inner.lo - outer.lo;
+  return rel <= outer.len && inner.len <= outer.len - rel;
 }
-inline uint64_t mul_checked(uint64_t a, uint64_t b) {
-  if (b && a > UINT64_MAX / b) throw RecordError("tensor shape overflow");
-  return a * b;
+// Sorted by start (then length), every range begins exactly where the previous
+// one ends, the first at 0: together they cover [0, end) once.
+inline bool ranges_tile_from_zero(std::vector<Range> v) {
+  std::sort(v.begin(), v.end(), [](const Range &x, const Range &y) { return x.lo < y.lo || (x.lo == y.lo && x.len < y.len); });
+  if (!v.empty() && v.front().lo != 0) return false;
+  return std::adjacent_find(v.begin(), v.end(), [](const Range &x, const Range &y) { return y.lo != x.lo + x.len; }) ==
+         v.end();
+}
+// No two non-empty ranges share a byte.
+inline bool ranges_disjoint(std::vector<Range> v) {
+  std::sort(v.begin(), v.end(), [](const Range &x, const Range &y) { return x.lo < y.lo || (x.lo == y.lo && x.len < y.len); });
+  return std::adjacent_find(v.begin(), v.end(), [](const Range &x, const Range &y) { return y.lo - x.lo < x.len; }) ==
+         v.end();
+}
+inline uint64_t sum_or_throw(uint64_t a, uint64_t b, const char *what) {
+  uint64_t r;
+  if (__builtin_add_overflow(a, b, &r)) throw RecordError(std::string(what) + ": 64-bit overflow");
+  return r;
+}
+inline uint64_t product_or_throw(uint64_t a, uint64_t b, const char *what) {
+  uint64_t r;
+  if (__builtin_mul_overflow(a, b, &r)) throw RecordError(std::string(what) + ": 64-bit overflow");
+  return r;
 }
 
 inline void pread_exact(int fd, void *dst, uint64_t n, uint64_t off) {
-  uint64_t done = 0;
-  while (done < n) {
+  for (uint64_t done = 0; done < n;) {
     const ssize_t r = pread(fd, static_cast<char *>(dst) + done, n - done, (off_t)(off + done));
     if (r < 0 && errno == EINTR) continue;
-    if (r <= 0) throw RecordError("short read");
+    if (r <= 0) throw RecordError(r == 0 ? "file ends before the bytes it must hold" : "read error");
     done += (uint64_t)r;
   }
 }
@@ -301,177 +320,221 @@ inline void pread_exact(int fd, void *dst, uint64_t n, uint64_t off) {
 struct Fd {
   int fd;
   explicit Fd(const std::string &p) : fd(open(p.c_str(), O_RDONLY | O_CLOEXEC)) {
-    if (fd < 0) throw RecordError("open failed: " + p);
+    if (fd < 0) throw RecordError("cannot open " + p);
   }
   ~Fd() { close(fd); }
   Fd(const Fd &) = delete;
   Fd &operator=(const Fd &) = delete;
+  uint64_t size() const {
+    struct stat st{};
+    if (fstat(fd, &st)) throw RecordError("cannot stat an open file");
+    return (uint64_t)st.st_size;
+  }
 };
 
-// Checkpoint tensor names as the engine binds them (engine/src/store.cpp:124-139).
-inline std::string normalize_tensor_name(std::string n) {
-  if (n.rfind("model.", 0) == 0) n.erase(0, 6);
-  auto swap_all = [&](const std::string &a, const std::string &b) {
-    for (size_t i = 0; (i = n.find(a, i)) != std::string::npos; i += b.size()) n.replace(i, a.size(), b);
+// ---- the safetensors checkpoint ------------------------------------------------
+// Where a checkpoint tensor's bytes are: its file, that file's full size, and
+// the absolute offset and length of the tensor in it.
+struct CkptTensor {
+  std::string name, path, dtype;
+  std::vector<uint64_t> shape;
+  uint64_t offset = 0, bytes = 0, file_bytes = 0;
+};
+
+// The tensor names the engine binds (engine/src/store.cpp:124-139): "model."
+// dropped, then each rewrite applied left to right over the whole name.
+inline std::string checkpoint_name(std::string n) {
+  static const std::string model = "model.", vision = "vision.";
+  if (n.compare(0, model.size(), model) == 0) n.erase(0, model.size());
+  struct Rewrite {
+    const char *from, *to;
+    bool outside_vision_only;
   };
-  swap_all("self_attn", "attn");
-  if (n.rfind("vision.", 0) != 0) swap_all("mlp", "ffn");
-  swap_all("weight_scale_inv", "scale");
-  swap_all("e_score_correction_bias", "bias");
+  static const Rewrite rewrites[] = {{"self_attn", "attn", false},
+                                     {"mlp", "ffn", true},
+                                     {"weight_scale_inv", "scale", false},
+                                     {"e_score_correction_bias", "bias", false}};
+  for (const Rewrite &rw : rewrites) {
+    if (rw.outside_vision_only && n.compare(0, vision.size(), vision) == 0) continue;
+    const std::string from = rw.from, to = rw.to;
+    std::string out;
+    size_t at = 0;
+    for (size_t hit; (hit = n.find(from, at)) != std::string::npos; at = hit + from.size()) out.append(n, at, hit - at).append(to);
+    n = out.append(n, at, std::string::npos);
+  }
   return n;
 }
 
-inline uint64_t dtype_bytes(const std::string &d) {
-  static const std::map<std::string, uint64_t> size = {
-      {"BOOL", 1}, {"U8", 1},  {"I8", 1},  {"I16", 2},     {"I32", 4},       {"I64", 8},     {"F16", 2},
-      {"BF16", 2}, {"F32", 4}, {"F64", 8}, {"F8_E4M3", 1}, {"F8_E4M3FN", 1}, {"F8_E8M0", 1}, {"F8_E8M0FNU", 1}};
-  auto it = size.find(d);
-  if (it == size.end()) throw RecordError("unsupported native dtype " + d);
+// Element sizes of the safetensors dtypes the engine accepts.
+inline uint64_t element_bytes(const std::string &dtype) {
+  static const std::unordered_map<std::string, uint64_t> table = {
+      {"BOOL", 1}, {"U8", 1}, {"I8", 1}, {"F8_E4M3", 1}, {"F8_E4M3FN", 1}, {"F8_E8M0", 1}, {"F8_E8M0FNU", 1},
+      {"I16", 2},  {"F16", 2}, {"BF16", 2}, {"I32", 4}, {"F32", 4}, {"I64", 8}, {"F64", 8}};
+  const auto it = table.find(dtype);
+  if (it == table.end()) throw RecordError("dtype " + dtype + " is not one the engine reads");
   return it->second;
 }
 
-// Opens model.safetensors.index.json under root and every shard it names: each
-// header is checked (length, dtype, shape x dtype == range, data ranges tile
-// [0, end) without gaps or overlap) and, with `complete`, each file must be
-// exactly 8 + header + data bytes long.
+// One shard: its header, where its data starts, and the size the file has when
+// complete (data start + the furthest tensor end).
+struct ShardScan {
+  JsonValue header;
+  uint64_t data_start = 0, file_bytes = 0;
+  std::string path;
+};
+
+// A shard's header must be 1 byte .. 128 MiB of JSON object; each tensor entry
+// (all but __metadata__) has a known dtype, an unsigned shape and a [lo, hi]
+// range whose length is the shape's byte count; the non-empty ranges cover
+// [0, end) exactly once. With `complete`, the file is data start + end bytes.
+inline ShardScan scan_shard(const std::string &path, bool complete) {
+  ShardScan sh;
+  sh.path = path;
+  Fd fd(path);
+  uint8_t le[8];
+  pread_exact(fd.fd, le, sizeof le, 0);
+  uint64_t header_len = 0;
+  for (int k = 7; k >= 0; --k) header_len = (header_len << 8) | le[k];
+  if (header_len == 0 || header_len > (128ull << 20)) throw RecordError("shard header length out of range: " + path);
+  std::string text(header_len, '\0');
+  pread_exact(fd.fd, &text[0], header_len, sizeof le);
+  sh.header = JsonReader(text).document();
+  if (sh.header.kind != JsonValue::Object) throw RecordError("shard header is not a JSON object: " + path);
+  std::vector<Range> data;
+  uint64_t end = 0;
+  for (const auto &entry : sh.header.members) {
+    if (entry.first == "__metadata__") continue;
+    const JsonValue &lohi = entry.second.at("data_offsets"), &shape = entry.second.at("shape");
+    if (lohi.kind != JsonValue::Array || lohi.items.size() != 2 || shape.kind != JsonValue::Array)
+      throw RecordError("tensor entry without a [lo, hi] range or a shape: " + entry.first);
+    const uint64_t lo = lohi.items[0].u64(), hi = lohi.items[1].u64();
+    if (hi < lo) throw RecordError("tensor range ends before it starts: " + entry.first);
+    uint64_t need = element_bytes(entry.second.at("dtype").text);
+    for (const auto &dim : shape.items) need = product_or_throw(need, dim.u64(), "tensor size");
+    if (need != hi - lo) throw RecordError("tensor range does not hold its shape and dtype: " + entry.first);
+    if (need) data.push_back(Range{lo, need});
+    end = std::max(end, hi);
+  }
+  if (!ranges_tile_from_zero(data)) throw RecordError("tensor data of the shard has gaps or overlaps: " + path);
+  sh.data_start = sum_or_throw(sizeof le, header_len, "shard data start");
+  sh.file_bytes = sum_or_throw(sh.data_start, end, "shard size");
+  const uint64_t have = fd.size();
+  if (complete && have != sh.file_bytes)
+    throw RecordError("shard is incomplete or was changed: " + path + " holds " + std::to_string(have) +
+                      " bytes, its header describes " + std::to_string(sh.file_bytes));
+  return sh;
+}
+
+// A shard file name from the index: one path component, relative.
+inline bool plain_file_name(const std::string &s) {
+  const std::filesystem::path p(s);
+  return !s.empty() && !p.is_absolute() && p == p.filename();
+}
+
+// Every tensor of the checkpoint under root (model.safetensors.index.json and
+// the shards it names, each scanned once), by its engine name; two source
+// names that become one engine name are an error.
 inline std::map<std::string, CkptTensor> open_checkpoint(const std::string &root_in, bool complete) {
   namespace fs = std::filesystem;
   const fs::path root = fs::canonical(root_in);
-  std::ifstream f(root / "model.safetensors.index.json");
-  if (!f) throw RecordError("cannot open " + (root / "model.safetensors.index.json").string());
-  std::stringstream ss;
-  ss << f.rdbuf();
-  const std::string index_text = ss.str();
+  const fs::path index_path = root / "model.safetensors.index.json";
+  std::ifstream f(index_path);
+  if (!f) throw RecordError("cannot open " + index_path.string());
+  const std::string index_text((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
   const JsonValue index = JsonReader(index_text).document();
-  const JsonValue &map = index.at("weight_map");
-  if (map.kind != JsonValue::Object) throw RecordError("weight_map is not an object");
-  struct Shard {
-    JsonValue header;
-    uint64_t start = 0, file_bytes = 0;
-    std::string path;
-  };
-  std::map<std::string, Shard> shards;
-  std::map<std::string, CkptTensor> out;
-  for (const auto &m : map.members) {
-    if (m.second.kind != JsonValue::String) throw RecordError("weight_map value is not a string");
-    const std::string &shard = m.second.text;
-    const fs::path rel(shard);
-    if (rel.is_absolute() || rel.filename() != rel) throw RecordError("unsafe shard path");
-    if (!shards.count(shard)) {
-      Shard sh;
-      sh.path = (root / rel).string();
-      Fd fd(sh.path);
-      uint8_t lb[8];
-      pread_exact(fd.fd, lb, 8, 0);
-      uint64_t len = 0;
-      for (int k = 0; k < 8; ++k) len |= (uint64_t)lb[k] << (8 * k);
-      if (!len || len > (128ull << 20)) throw RecordError("invalid safetensors header length");
-      std::string raw(len, '\0');
-      pread_exact(fd.fd, raw.data(), len, 8);
-      sh.header = JsonReader(raw).document();
-      if (sh.header.kind != JsonValue::Object) throw RecordError("safetensors header is not an object");
-      sh.start = add_checked(8, len);
-      uint64_t end = 0;
-      std::vector<std::pair<uint64_t, uint64_t>> ranges;
-      for (const auto &t : sh.header.members) {
-        if (t.first == "__metadata__") continue;
-        const JsonValue &r = t.second.at("data_offsets");
-        if (r.items.size() != 2 || r.items[1].u64() < r.items[0].u64()) throw RecordError("invalid tensor range");
-        uint64_t bytes = dtype_bytes(t.second.at("dtype").text);
-        for (const auto &d : t.second.at("shape").items) bytes = mul_checked(bytes, d.u64());
-        const uint64_t lo = r.items[0].u64(), hi = r.items[1].u64();
-        if (bytes != hi - lo) throw RecordError("tensor byte/shape mismatch: " + t.first);
-        if (bytes) ranges.push_back({lo, hi});
-        end = std::max(end, hi);
-      }
-      std::sort(ranges.begin(), ranges.end());
-      uint64_t cursor = 0;
-      for (const auto &r : ranges) {
-        if (r.first != cursor) throw RecordError("overlapping or gapped tensor data");
-        cursor = r.second;
-      }
-      struct stat st{};
-      if (fstat(fd.fd, &st)) throw RecordError("fstat failed");
-      sh.file_bytes = add_checked(sh.start, end);
-      if (complete && (uint64_t)st.st_size != sh.file_bytes) throw RecordError("incomplete/changed shard: " + shard);
-      shards.emplace(shard, std::move(sh));
-    }
-    const Shard &sh = shards.at(shard);
-    const JsonValue &d = sh.header.at(m.first);
-    const JsonValue &r = d.at("data_offsets");
+  const JsonValue &weight_map = index.at("weight_map");
+  if (weight_map.kind != JsonValue::Object) throw RecordError("weight_map must be a JSON object");
+  std::map<std::string, ShardScan> scanned;
+  std::map<std::string, CkptTensor> tensors;
+  for (const auto &entry : weight_map.members) {
+    if (entry.second.kind != JsonValue::String || !plain_file_name(entry.second.text))
+      throw RecordError("weight_map names a shard outside the checkpoint directory: " + entry.first);
+    const std::string &shard = entry.second.text;
+    auto it = scanned.find(shard);
+    if (it == scanned.end()) it = scanned.emplace(shard, scan_shard((root / shard).string(), complete)).first;
+    const ShardScan &sh = it->second;
+    const JsonValue &desc = sh.header.at(entry.first);
+    const JsonValue &lohi = desc.at("data_offsets");
     CkptTensor t;
-    t.name = normalize_tensor_name(m.first);
+    t.name = checkpoint_name(entry.first);
     t.path = sh.path;
-    t.dtype = d.at("dtype").text;
-    for (const auto &x : d.at("shape").items) t.shape.push_back(x.u64());
-    t.offset = add_checked(sh.start, r.items.at(0).u64());
-    t.bytes = r.items.at(1).u64() - r.items.at(0).u64();
+    t.dtype = desc.at("dtype").text;
+    for (const auto &dim : desc.at("shape").items) t.shape.push_back(dim.u64());
+    t.offset = sum_or_throw(sh.data_start, lohi.items.at(0).u64(), "tensor offset");
+    t.bytes = lohi.items.at(1).u64() - lohi.items.at(0).u64();
     t.file_bytes = sh.file_bytes;
-    const std::string name = t.name;
-    if (!out.emplace(name, std::move(t)).second) throw RecordError("duplicate normalized name: " + name);
+    if (tensors.count(t.name)) throw RecordError("two checkpoint tensors share the engine name " + t.name);
+    tensors.emplace(t.name, std::move(t));
   }
-  return out;
+  return tensors;
 }
 
-// Record extents: non-empty, inside the record, sorted without overlap.
-inline void check_spans(uint64_t size, std::vector<std::pair<uint64_t, uint64_t>> spans) {
-  if (!size || spans.empty()) throw RecordError("empty expert record/spans");
-  std::sort(spans.begin(), spans.end());
-  uint64_t end = 0;
-  for (const auto &s : spans) {
-    if (!s.second || s.first < end || s.first > size || s.second > size - s.first)
-      throw RecordError("overlapping/out-of-bounds expert read spans");
-    end = s.first + s.second;
+// ---- records against the checkpoint ------------------------------------------
+// A record's buffer geometry: some bytes and extents, each extent non-empty,
+// inside the buffer, and no two extents writing the same byte.
+inline void check_destinations(const ExpertRecord &r) {
+  if (r.bytes == 0 || r.extents.empty()) throw RecordError("expert record without bytes or extents");
+  std::vector<Range> dst;
+  for (const auto &e : r.extents) {
+    const Range d{e.dst_offset, e.bytes};
+    if (d.len == 0 || !range_within(Range{0, r.bytes}, d))
+      throw RecordError("expert extent is empty or lies outside its record buffer");
+    dst.push_back(d);
   }
+  if (!ranges_disjoint(dst)) throw RecordError("expert extents overlap in the record buffer");
 }
 
-inline std::string expert_prefix(uint32_t id) {
-  const uint32_t base = kTargetLayers * kTargetExperts;
-  const uint32_t layer = id < base ? id / kTargetExperts : kTargetLayers + (id - base) / kDrafterExperts;
-  const uint32_t e = id < base ? id % kTargetExperts : (id - base) % kDrafterExperts;
-  return (layer < kTargetLayers ? "layers." + std::to_string(layer) : "mtp." + std::to_string(layer - kTargetLayers)) +
-         ".ffn.experts." + std::to_string(e);
+// The checkpoint name of one of a record's six tensors (ids as in
+// components/moe/include/ds41/store.hpp:16).
+inline std::string expert_tensor_name(uint32_t id, int field) {
+  static const char *kField[6] = {"w1.weight", "w1.scale", "w3.weight", "w3.scale", "w2.weight", "w2.scale"};
+  constexpr uint32_t target_ids = kTargetLayers * kTargetExperts;
+  const bool drafter = id >= target_ids;
+  const uint32_t group = drafter ? (id - target_ids) / kDrafterExperts : id / kTargetExperts;
+  const uint32_t expert = drafter ? (id - target_ids) % kDrafterExperts : id % kTargetExperts;
+  return std::string(drafter ? "mtp." : "layers.") + std::to_string(group) + ".ffn.experts." +
+         std::to_string(expert) + "." + kField[field];
 }
 
-// Every record must read exactly the checkpoint's six expert tensors: each
-// view has the tensor's byte count and lies inside the required part of an
-// extent of the tensor's own file at the tensor's own file offset, and every
-// extent serves at least one view.
+// An extent serves a view when the view's destination lies within the bytes
+// the extent must deliver and the file position it maps the view to is the
+// tensor's own place: same file, same file size, same offset.
+inline bool extent_serves(const RecordExtent &e, const RecordView &v, const CkptTensor &t) {
+  if (e.path != t.path || e.expected_file_bytes != t.file_bytes) return false;
+  if (!range_within(Range{e.dst_offset, e.need()}, Range{v.offset, v.bytes})) return false;
+  return e.file_offset + (v.offset - e.dst_offset) == t.offset;
+}
+
+// The engine's checks before any read (engine/src/forward.cu:1781-1832): per
+// record, each extent's required bytes fit the extent and its file, the buffer
+// geometry holds, the id is a valid expert seen once; then every view has its
+// tensor's byte count and is served by some extent, and every extent serves
+// some view.
 inline void validate_records(const std::vector<ExpertRecord> &records,
                              const std::map<std::string, CkptTensor> &ckpt) {
-  static const char *kField[6] = {"w1.weight", "w1.scale", "w3.weight", "w3.scale", "w2.weight", "w2.scale"};
-  std::vector<char> seen(kExpertIds, 0);
+  std::vector<bool> seen(kExpertIds, false);
   for (const auto &r : records) {
-    std::vector<std::pair<uint64_t, uint64_t>> spans;
     for (const auto &e : r.extents) {
-      if (e.need() > e.bytes || e.file_offset > e.expected_file_bytes ||
-          e.need() > e.expected_file_bytes - e.file_offset)
-        throw RecordError("invalid required expert span/file coverage");
-      spans.emplace_back(e.dst_offset, e.bytes);
+      if (e.need() > e.bytes || !range_within(Range{0, e.expected_file_bytes}, Range{e.file_offset, e.need()}))
+        throw RecordError("expert extent's required bytes exceed the extent or run past its file");
     }
-    check_spans(r.bytes, spans);
-    if (r.id >= kExpertIds || seen[r.id]) throw RecordError("expert manifest duplicate/id");
-    seen[r.id] = 1;
-    const std::string prefix = expert_prefix(r.id);
-    std::vector<char> used(r.extents.size(), 0);
+    check_destinations(r);
+    if (r.id >= kExpertIds || seen[r.id]) throw RecordError("expert id out of range or listed twice");
+    seen[r.id] = true;
+    std::vector<bool> serving(r.extents.size(), false);
     for (int f = 0; f < 6; ++f) {
-      auto it = ckpt.find(prefix + "." + kField[f]);
-      if (it == ckpt.end()) throw RecordError("missing checkpoint tensor " + prefix + "." + kField[f]);
+      const std::string name = expert_tensor_name(r.id, f);
+      const auto it = ckpt.find(name);
+      if (it == ckpt.end()) throw RecordError("the checkpoint has no tensor " + name);
       const CkptTensor &t = it->second;
-      const RecordView &v = r.view[f];
-      if (v.bytes != t.bytes) throw RecordError("expert view byte mismatch");
-      bool found = false;
-      for (size_t k = 0; k < r.extents.size(); ++k) {
-        const RecordExtent &e = r.extents[k];
-        const uint64_t cover = e.need();
-        if (v.offset >= e.dst_offset && v.offset - e.dst_offset <= cover && v.bytes <= cover - (v.offset - e.dst_offset) &&
-            e.path == t.path && e.expected_file_bytes == t.file_bytes &&
-            e.file_offset + (v.offset - e.dst_offset) == t.offset)
-          found = used[k] = 1;
-      }
-      if (!found) throw RecordError("expert view does not match verified native tensor/required extent coverage: " + prefix);
+      if (r.view[f].bytes != t.bytes) throw RecordError("record view size differs from tensor " + name);
+      bool served = false;
+      for (size_t k = 0; k < r.extents.size(); ++k)
+        if (extent_serves(r.extents[k], r.view[f], t)) served = serving[k] = true;
+      if (!served) throw RecordError("no extent reads tensor " + name + " from its place in the checkpoint");
     }
-    if (std::find(used.begin(), used.end(), 0) != used.end()) throw RecordError("extraneous expert read span");
+    if (std::find(serving.begin(), serving.end(), false) != serving.end())
+      throw RecordError("expert record has an extent that reads none of its tensors");
   }
 }
 
@@ -481,9 +544,7 @@ inline void validate_records(const std::vector<ExpertRecord> &records,
 inline void read_record(const ExpertRecord &r, uint8_t *dst) {
   for (const auto &e : r.extents) {
     Fd fd(e.path);
-    struct stat st{};
-    if (fstat(fd.fd, &st)) throw RecordError("fstat failed");
-    if ((uint64_t)st.st_size != e.expected_file_bytes) throw RecordError("expert file size changed: " + e.path);
+    if (fd.size() != e.expected_file_bytes) throw RecordError("expert file size changed: " + e.path);
     uint64_t done = 0;
     while (done < e.bytes) {
       const ssize_t n = pread(fd.fd, dst + e.dst_offset + done, e.bytes - done, (off_t)(e.file_offset + done));

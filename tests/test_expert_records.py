@@ -215,6 +215,9 @@ MUTATIONS = {
     "duplicate_id": lambda recs: recs[1].__setitem__("id", recs[0]["id"]),
     "absent_expert": lambda recs: recs[0].__setitem__("id", expert_id(5, 5)),
     "span_past_record": lambda recs: recs[0].__setitem__("bytes", recs[0]["extents"][-1][3] + 8),
+    "empty_extent": lambda recs: recs[1]["extents"].append(
+        [recs[1]["extents"][0][0], 0, 0, recs[1]["bytes"], 0, recs[1]["extents"][0][5]]),
+    "required_past_file": lambda recs: recs[4]["extents"][0].__setitem__(4, recs[4]["extents"][0][5] + 1),
 }
 
 
@@ -261,3 +264,47 @@ def test_checkpoint_checks(tmp_path):
         open(shard, "wb").write(struct.pack("<Q", len(body)) + body + raw[8 + n:])
         with pytest.raises(ValueError):
             rs.validate(root, complete=False)
+
+
+def _rewrite_index(root, fn):
+    p = os.path.join(root, "model.safetensors.index.json")
+    idx = json.load(open(p))
+    fn(idx["weight_map"])
+    json.dump(idx, open(p, "w"))
+
+
+@pytest.mark.parametrize("case", ["unsafe_path", "absolute_path", "duplicate_engine_name", "header_too_long"])
+def test_checkpoint_rejects(tmp_path, case):
+    """The checkpoint index and shard checks of engine/src/store.cpp:140-217 (as rules, not text): shard
+    names stay inside the checkpoint directory, two source names may not map to one engine name, and a
+    header length must be 1 .. 128 MiB."""
+    root = str(tmp_path / "ckpt")
+    os.makedirs(root)
+    make_checkpoint(root)
+    manifest = str(tmp_path / "records.tsv")
+    write_manifest(root, manifest)
+    rs = G.Records(manifest)
+    rs.validate(root)
+    if case == "unsafe_path":
+        _rewrite_index(root, lambda m: m.__setitem__(next(iter(m)), "../" + m[next(iter(m))]))
+    elif case == "absolute_path":
+        _rewrite_index(root, lambda m: m.__setitem__(next(iter(m)), os.path.join(root, m[next(iter(m))])))
+    elif case == "duplicate_engine_name":
+        # "model.layers.0.mlp.gate.weight" normalises to "layers.0.ffn.gate.weight": add the second spelling
+        shard = os.path.join(root, "model-00002-of-00002.safetensors")
+        raw = open(shard, "rb").read()
+        n, = struct.unpack("<Q", raw[:8])
+        hdr = json.loads(raw[8:8 + n])
+        hdr["layers.0.ffn.gate.weight"] = dict(hdr["model.layers.0.mlp.gate.weight"])
+        hdr["layers.0.ffn.gate.weight"]["data_offsets"] = [0, 0]
+        hdr["layers.0.ffn.gate.weight"]["shape"] = [0]
+        body = json.dumps(hdr).encode()
+        open(shard, "wb").write(struct.pack("<Q", len(body)) + body + raw[8 + n:])
+        _rewrite_index(root, lambda m: m.__setitem__("layers.0.ffn.gate.weight", "model-00002-of-00002.safetensors"))
+    else:
+        shard = os.path.join(root, "model-00001-of-00002.safetensors")
+        raw = bytearray(open(shard, "rb").read())
+        raw[:8] = struct.pack("<Q", (128 << 20) + 1)
+        open(shard, "wb").write(bytes(raw))
+    with pytest.raises(ValueError):
+        rs.validate(root)
