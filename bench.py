@@ -38,6 +38,10 @@ PEAK_FP4_TFLOPS = 10100.0
 # (profiles/verify_layer_config1_traffic.md); the algorithmic figure at that U is 304,923,000 B.
 GATE_UP_TRAFFIC_BYTES = 323_432_000
 METRIC = "verify tokens/s per MTP step (T=1+k); MoE HBM GB/s as % of 8 TB/s peak"
+# Expert weight layout of the configs[1] and configs[4] legs: 1 = tiled (ds41_expert_slab_tile, the MFMA
+# operand order), 0 = the checkpoint's row-major layout. The synthetic weights are uniform random bytes,
+# which read as uniform e2m1 codes in either layout.
+LAYOUT = {"weights": 1}
 DRAFT = 1
 
 
@@ -130,6 +134,8 @@ def bench_layer(gpu, steps, warmup, cpu_seconds, no_cpu, fp8_legs=True):
     ids_dev = torch.empty((pool, T, K), dtype=torch.int32, device=gpu)
     w_dev = torch.empty((pool, T, K), dtype=torch.float32, device=gpu)
     layer_args = [G.make_layer_args(x_pool[i], wg, bias, table, 0, E, T, H, I, E, K, y, ws) for i in range(pool)]
+    for a in layer_args:
+        a.weight_layout = LAYOUT["weights"]
     stream = torch.cuda.current_stream()
 
     # unique routed experts per pool entry (bytes actually streamed per step), and the routing
@@ -137,6 +143,7 @@ def bench_layer(gpu, steps, warmup, cpu_seconds, no_cpu, fp8_legs=True):
     for i in range(pool):
         a = G.make_layer_args(x_pool[i], wg, bias, table, 0, E, T, H, I, E, K, y, ws, ids_out=ids_dev[i],
                               weights_out=w_dev[i])
+        a.weight_layout = LAYOUT["weights"]
         G.moe_layer(a, stream)
         uniq.append(len(G.layer_plan(ws, T, H, I, E, K)))
     torch.cuda.synchronize()
@@ -180,6 +187,7 @@ def bench_layer(gpu, steps, warmup, cpu_seconds, no_cpu, fp8_legs=True):
     wss = [torch.zeros_like(ws) for _ in range(pool)]
     prep = [G.make_layer_args(x_pool[i], wg, bias, table, 0, E, T, H, I, E, K, y, wss[i]) for i in range(pool)]
     for a in prep:
+        a.weight_layout = LAYOUT["weights"]
         G.moe_layer(a, stream)
     reps = max(steps // pool, 1)
     launch_us = {}
@@ -233,6 +241,7 @@ def bench_layer(gpu, steps, warmup, cpu_seconds, no_cpu, fp8_legs=True):
     res = {
         "workload": "configs[1]: one MoE layer decode verify, T=4 (1+3 MTP drafts), hidden 4096, 384 routed "
                     "experts (I=2880, MXFP4) top-6 + 1 shared, all HBM-resident",
+        "weight_layout": "tiled" if LAYOUT["weights"] else "row-major",
         "steps": steps, "warmup": warmup, "value": T / (ms_per_step * 1e-3), "unit": "tokens/s",
         "us_per_layer": ms_per_step * 1e3, "mean_unique_experts": mean_u,
         "hbm_gbps": layer_gbps, "hbm_frac": layer_gbps / PEAK_HBM_GBPS,
@@ -818,7 +827,7 @@ def bench_stack(gpu, steps, warmup, fill_steps, side_steps, cpu_seconds, no_cpu,
     resident_gb = torch.cuda.memory_allocated() / 1e9
     log(f"stack: {L} layers x ({RES}+1 resident, {NH} host) experts ready in {time.perf_counter() - t0:.1f} s, "
         f"HBM in use {resident_gb:.1f} GB")
-    stack = G.VerifyStack(layers, T, H, I, E, K, slab_bytes=slab)
+    stack = G.VerifyStack(layers, T, H, I, E, K, slab_bytes=slab, weight_layout=LAYOUT["weights"])
     rng = np.random.default_rng(seed)
     pool = 16
     xs = torch.randn((pool, T, H), generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
@@ -942,6 +951,7 @@ def main():
     ap.add_argument("--stack-side-steps", type=int, default=200, help="steps of the no-cache Zipf leg")
     ap.add_argument("--fp8-shared", type=int, default=1, help="0 skips the FP8 shared-expert leg")
     ap.add_argument("--legs", default="all", help="comma list of expert,layer,accept,prefill,drafter,stack")
+    ap.add_argument("--weight-layout", type=int, default=1, help="1 tiled expert weights, 0 row-major")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -959,6 +969,7 @@ def main():
               "is a single-GPU workload here and multi-GPU sharding is design-only.", file=sys.stderr)
         sys.exit(2)
     legs = set(("expert,layer,accept,prefill,drafter,stack" if args.legs == "all" else args.legs).split(","))
+    LAYOUT["weights"] = args.weight_layout
 
     import torch
     gpu = torch.device("cuda:0")
@@ -1006,6 +1017,7 @@ def main():
                                "warm from the zipf_cache_fill leg of this run (reported in step40)",
                    "tokens": 4, "layers": 40, "hidden": 4096, "inter": 2880, "experts": 384, "topk": 6,
                    "resident_per_layer": 320, "host_tier_per_layer": 64,
+                   "weight_layout": "tiled" if LAYOUT["weights"] else "row-major",
                    "cache_slots": head["cache"]["slots"] if head else None},
         "hbm_gbps": head["hbm_gbps"] if head else None, "hbm_frac": head["hbm_frac"] if head else None,
         "roofline": dict(layer["roofline"], measured_on="configs[1] layer launches of this run (the gate/up/act "

@@ -335,12 +335,24 @@ __device__ __forceinline__ void split_chunk(const uint4 &lo, const uint4 &hi, v8
 }
 
 
+// Tiled weights (ds41_expert_slab_tile): the 16-byte K32 pieces of an MXFP4
+// matrix [N][K/2] stored in the MFMA B-operand order, piece (row n, group g) at
+// (n / 16) * (K / 32) * 256 + g * 256 + (n % 16) * 16. A wave's chunk load (16
+// rows x 4 groups) is then one contiguous kilobyte, read once, with
+// non-temporal loads. N % 16 == 0. The row-major reference layout has the
+// piece at n * K / 2 + g * 16.
+template <bool Tiled>
+__device__ __forceinline__ const uint8_t *weight_row(const uint8_t *w, int row, int K) {
+  return Tiled ? w + (size_t)(row >> 4) * ((size_t)K << 3) + (size_t)(row & 15) * 16 : w + (size_t)row * (size_t)(K >> 1);
+}
+
 // GScale: the weight scales come from global memory instead of an LDS row.
 // With each batch's weights a lane loads its channel's 32 scale bytes of that
 // batch (8 chunks x 4 groups; dword u holds chunk u's four groups) and takes
 // byte kb of each dword. Requires U == 8 and k % 1024 == 0 (whole batches).
 // Frees the workgroup's LDS of the weight scales.
-template <int U, bool Aligned16, bool GScale = false>
+// Tiled: `wrow` from weight_row<true>; pieces are 256 bytes apart.
+template <int U, bool Aligned16, bool GScale = false, bool Tiled = false>
 struct Gemv16 {
   const uint8_t *w;  // weight row
   const uint8_t *gs; // GScale: this lane's channel's scale row
@@ -356,6 +368,10 @@ struct Gemv16 {
     const int cc = c < nch ? c : nch - 1;
     int g = 4 * cc + kb;
     g = g < ng ? g : ng - 1;
+    if (Tiled) {  // each kilobyte block is read by this one instruction: no reuse to keep in the caches
+      const u32x4 v = __builtin_nontemporal_load((global_u4)(w + 256 * g));
+      return make_uint4(v.x, v.y, v.z, v.w);
+    }
     const uint8_t *p = w + 16 * g;
     if (Aligned16) {
       const u32x4 v = *(global_u4)(p);

@@ -43,7 +43,7 @@ class MoeLayerArgs(ctypes.Structure):
                 ("workspace_bytes", ctypes.c_size_t), ("ids_out", ctypes.c_void_p),
                 ("weights_out", ctypes.c_void_p), ("logits_out", ctypes.c_void_p),
                 ("stage_events", ctypes.c_void_p), ("stage_mask", ctypes.c_uint32),
-                ("shared_fp8", ctypes.c_void_p)]
+                ("shared_fp8", ctypes.c_void_p), ("weight_layout", ctypes.c_int32)]
 
 
 class MoePrefillArgs(ctypes.Structure):
@@ -70,7 +70,7 @@ class StackDesc(ctypes.Structure):
     _fields_ = [("layers", ctypes.c_int32), ("max_tokens", ctypes.c_int32), ("hidden", ctypes.c_int32),
                 ("inter", ctypes.c_int32), ("n_experts", ctypes.c_int32), ("topk", ctypes.c_int32),
                 ("score_mode", ctypes.c_int32), ("route_scale", ctypes.c_float), ("swiglu_limit", ctypes.c_float),
-                ("layer", ctypes.POINTER(StackLayer))]
+                ("layer", ctypes.POINTER(StackLayer)), ("weight_layout", ctypes.c_int32)]
 
 
 class StackStats(ctypes.Structure):
@@ -510,6 +510,18 @@ def layer_plan(workspace, T, H, I, E, K):
 
 
 # ---- verify step through a layer stack with a host expert tier ----------------------
+def slab_tile(src, dst, hidden, inter, count, stream=None):
+    """ds41_expert_slab_tile: count canonical slabs (device uint8 tensors) with tiled weights."""
+    check(lib().ds41_expert_slab_tile(_p(src), _p(dst), hidden, inter, count, _stream(stream)), "ds41_expert_slab_tile")
+
+
+def slab_tile_host(src, dst, hidden, inter, count):
+    """ds41_expert_slab_tile_host on host uint8 tensors or numpy arrays."""
+    def ptr(a):
+        return ctypes.c_void_p(a.data_ptr() if hasattr(a, "data_ptr") else a.ctypes.data)
+    check(lib().ds41_expert_slab_tile_host(ptr(src), ptr(dst), hidden, inter, count), "ds41_expert_slab_tile_host")
+
+
 def slab_layout(hidden, inter):
     """Canonical expert slab: ([gate, gate_scale, up, up_scale, down, down_scale] byte offsets, slab bytes)."""
     out = ExpertLayout()
@@ -563,7 +575,7 @@ class VerifyStack:
     tensor of host_slab_count slabs). The tensors must outlive the stack."""
 
     def __init__(self, layers, max_tokens, hidden, inter, n_experts, topk, score_mode=0, route_scale=1.5,
-                 swiglu_limit=10.0, slab_bytes=None):
+                 swiglu_limit=10.0, slab_bytes=None, weight_layout=0):
         arr = (StackLayer * len(layers))()
         for i, d in enumerate(layers):
             arr[i].router_w, arr[i].router_bias = d["router_w"].data_ptr(), d["router_bias"].data_ptr()
@@ -575,7 +587,7 @@ class VerifyStack:
             arr[i].host_slab_count = 0 if hs is None else hs.numel() // slab_bytes
         self._arr = arr
         desc = StackDesc(len(layers), max_tokens, hidden, inter, n_experts, topk, score_mode, route_scale,
-                         swiglu_limit, arr)
+                         swiglu_limit, arr, weight_layout)
         self.handle = ctypes.c_void_p(0)
         check(lib().ds41_verify_stack_create(ctypes.byref(desc), ctypes.byref(self.handle)),
               "ds41_verify_stack_create")

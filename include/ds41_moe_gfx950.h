@@ -160,6 +160,10 @@ typedef struct ds41_moe_layer_args {
                                      ([rows/32][cols/32]); W8A8 with MXFP8 activations
                                      (components/dense/src/dense.cu:37-91, batch.inc:330-335
                                      bshared). Requires shared_index < 0. */
+  int32_t weight_layout;          /* 0: the table's MXFP4 weights are row-major [N][K/2] (the
+                                     checkpoint's layout); 1: tiled by ds41_expert_slab_tile (the MFMA
+                                     operand order, read as contiguous kilobytes); scales are row-major
+                                     either way */
 } ds41_moe_layer_args;
 size_t ds41_moe_layer_workspace_bytes(int tokens, int hidden, int inter, int n_experts,
                                       int topk);
@@ -246,6 +250,14 @@ typedef struct ds41_expert_layout {
   uint64_t bytes;
 } ds41_expert_layout;
 int ds41_expert_slab_layout(int hidden, int inter, ds41_expert_layout *out);
+/* No counterpart in the reference. Copies `count` consecutive canonical slabs from `in` to `out`
+ * (distinct, 256-byte aligned) with the three weight tensors tiled in the MFMA operand order: the
+ * 16-byte piece of row n, K32 group g of a [N][K/2] tensor goes to
+ * (n / 16) * (K / 32) * 256 + g * 256 + (n % 16) * 16. The slab size is unchanged. Tiled slabs let
+ * each GEMV load instruction read one contiguous kilobyte (weight_layout 1). ds41_expert_slab_tile:
+ * device memory, on `stream`; _host: host memory, synchronous. */
+int ds41_expert_slab_tile(const void *in, void *out, int hidden, int inter, int count, void *stream);
+int ds41_expert_slab_tile_host(const void *in, void *out, int hidden, int inter, int count);
 
 /* One layer of the stack. Routed expert id e is table[expert_base + e]; the
  * shared expert is table[shared_index] (< 0: none). Residency (the reference's
@@ -269,6 +281,8 @@ typedef struct ds41_stack_desc {
   int32_t layers, max_tokens, hidden, inter, n_experts, topk, score_mode;
   float route_scale, swiglu_limit;
   const ds41_stack_layer *layer;   /* host array [layers], copied at create */
+  int32_t weight_layout;           /* as ds41_moe_layer_args.weight_layout, for every table, host and
+                                      cached slab of the stack */
 } ds41_stack_desc;
 
 /* Cumulative counters of the layers that have a host tier (read back each layer). */

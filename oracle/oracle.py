@@ -298,17 +298,19 @@ def _expert_struct(e):
     return Expert(*[e[f].ctypes.data for f in ("gate", "gate_scale", "up", "up_scale", "down", "down_scale")])
 
 
-def expert_ffn(e, xq, xs, route_w, hidden, inter, limit=10.0):
-    """One expert on quantised rows -> bf16 bits [m][hidden]."""
+def expert_ffn(e, xq, xs, route_w, hidden, inter, limit=10.0, return_acc=False):
+    """One expert on quantised rows -> bf16 bits [m][hidden] (and, with return_acc, the down
+    projection's fp32 accumulators [m][hidden] that round to them)."""
     m = xq.shape[0]
     out = np.empty((m, hidden), np.uint16)
+    acc = np.empty((m, hidden), np.float32) if return_acc else None
     es = _expert_struct(e)
     wv = None if route_w is None else np.ascontiguousarray(route_w, np.float32)
     rc = lib().oracle_expert_ffn(ctypes.byref(es), _ptr(np.ascontiguousarray(xq)), _ptr(np.ascontiguousarray(xs)),
-                                 _ptr(wv), m, hidden, inter, ctypes.c_float(limit), _ptr(out), ctypes.c_void_p(0))
+                                 _ptr(wv), m, hidden, inter, ctypes.c_float(limit), _ptr(out), _ptr(acc))
     if rc:
         raise ValueError("oracle_expert_ffn")
-    return out
+    return (out, acc) if return_acc else out
 
 
 def dense_fp8(w, ws, xq, xs, m, n, k):
