@@ -392,6 +392,12 @@ struct Gemv16 {
     S[1] = make_uint4(v1.x, v1.y, v1.z, v1.w);
   }
   __device__ __forceinline__ Gemv16(const uint8_t *wrow, int k, const uint8_t *gscale_row = nullptr) {
+    begin(wrow, k, gscale_row);
+  }
+  // Unbound: begin() names the row and issues its first batch (for a caller that
+  // starts the stream before it knows the row is needed, or across a branch).
+  __device__ __forceinline__ Gemv16() {}
+  __device__ __forceinline__ void begin(const uint8_t *wrow, int k, const uint8_t *gscale_row = nullptr) {
     kb = (threadIdx.x & 63) >> 4;
     w = wrow;
     gs = gscale_row;
