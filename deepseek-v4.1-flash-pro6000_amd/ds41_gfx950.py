@@ -98,6 +98,8 @@ def lib():
         _lib = ctypes.CDLL(LIB_PATH)
         _lib.ds41_moe_layer_workspace_bytes.restype = ctypes.c_size_t
         _lib.ds41_moe_layer_noalloc_max_bytes.restype = ctypes.c_size_t
+        _lib.ds41_drift_completed_tokens.restype = ctypes.c_uint64
+        _lib.ds41_drift_error.restype = ctypes.c_char_p
         _lib.ds41_moe_prefill_workspace_bytes.restype = ctypes.c_size_t
         _lib.ds41_gfx950_version.restype = ctypes.c_char_p
         _lib.ds41_spark_accept_workspace_bytes.restype = ctypes.c_size_t
@@ -746,6 +748,42 @@ class ExpertPool:
     def reset_history(self):
         return lib().ds41_pool_reset_history(self.h)
 
+    def retain(self, e):
+        """ds41_pool_retain -> (rc, token handle or None); drop it with token_release()."""
+        t = ctypes.c_void_p(0)
+        rc = lib().ds41_pool_retain(self.h, ctypes.c_uint32(e), ctypes.byref(t))
+        return rc, (t.value if rc == 0 else None)
+
+    @staticmethod
+    def token_release(token):
+        return lib().ds41_pool_token_release(ctypes.c_void_p(token))
+
+    def reserve(self, target, wanted=()):
+        out = (PoolAllocation * max(int(target), 1))()
+        rc = lib().ds41_pool_reserve(self.h, int(target), _u32(list(wanted)), len(wanted), out)
+        return rc, [(a.id, a.slot, bool(a.hit), a.evicted) for a in out[:max(rc, 0)]]
+
+    def drained(self, slot):
+        return lib().ds41_pool_drained(self.h, int(slot))
+
+    def peer(self, other, host):
+        return lib().ds41_pool_peer(self.h, other.h if other is not None else None, int(host))
+
+    def exclusive(self, on):
+        return lib().ds41_pool_exclusive(self.h, int(on))
+
+    def decay_interval(self, d):
+        return lib().ds41_pool_decay_interval(self.h, int(d))
+
+    def fast_minima(self, on):
+        return lib().ds41_pool_fast_minima(self.h, int(on))
+
+    def switch_target_layer(self, placement, layer):
+        return lib().ds41_pool_switch_target_layer(self.h, ctypes.byref(placement), int(layer))
+
+    def late(self, layer):
+        return lib().ds41_pool_late(self.h, int(layer))
+
     def error(self):
         return lib().ds41_pool_error(self.h).decode()
 
@@ -753,6 +791,37 @@ class ExpertPool:
         try:
             if self.h:
                 lib().ds41_pool_destroy(self.h)
+        except Exception:
+            pass
+
+
+class DriftControl:
+    """ds41_drift_*: the width-one drift controller over a VRAM pool and its RAM pool (keeps both
+    pools and the placement alive)."""
+
+    def __init__(self, placement, vram, ram):
+        self.h = ctypes.c_void_p(0)
+        self._keep = (placement, vram, ram)
+        err = ctypes.create_string_buffer(256)
+        self.rc = lib().ds41_drift_create(ctypes.byref(placement), vram.h, ram.h, ctypes.byref(self.h), err, 256)
+        self.msg = err.value.decode()
+
+    def before(self, ids):
+        return lib().ds41_drift_before(self.h, _u32(ids), len(ids))
+
+    def after(self, ids):
+        return lib().ds41_drift_after(self.h, _u32(ids), len(ids))
+
+    def active(self):
+        return lib().ds41_drift_active(self.h)
+
+    def completed_tokens(self):
+        return lib().ds41_drift_completed_tokens(self.h)
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().ds41_drift_destroy(self.h)
         except Exception:
             pass
 

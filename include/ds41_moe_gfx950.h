@@ -399,6 +399,48 @@ int ds41_pool_pin(void *pool, uint32_t id);
 int ds41_pool_unpin(void *pool, uint32_t id);
 int ds41_pool_residency(void *pool, uint32_t id);                     /* slot or -1 */
 int ds41_pool_reset_history(void *pool);
+/* SlotPool::retain (store.hpp:99-101): a token of the expert's slot contents; while any token of
+ * the current occupant lives, the slot is neither evicted nor counted as usable. The token is
+ * released with ds41_pool_token_release, which is thread-safe, never calls the pool and stays
+ * valid after ds41_pool_destroy. */
+int ds41_pool_retain(void *pool, uint32_t id, void **token);
+int ds41_pool_token_release(void *token);
+/* SlotPool::reserve / drained (store.hpp:102-106, store.cpp:130-152), soft pools only: evicts
+ * policy victims (never wanted, pinned, leased or retained) into draining slots until empty +
+ * draining slots reach `target`; out (at least `target` entries) gets one allocation per victim
+ * with evicted = its id; returns their count. A draining slot has no occupant and is not
+ * allocatable until ds41_pool_drained(slot). */
+int ds41_pool_reserve(void *pool, int target, const uint32_t *wanted, int n_wanted,
+                      ds41_pool_allocation *out);
+int ds41_pool_drained(void *pool, int slot);
+/* SlotPool::peer / exclusive / decay_interval / fast_minima / switch_target_layer
+ * (store.hpp:88-92,107, store.cpp:162-190). The peer (NULL clears it) must share the id space
+ * and outlive its use; host != 0 marks this pool as the host tier. Victims are ordered by a score:
+ * the LFU count, 0 for an exclusive host pool's peer-resident experts, and in a late target layer
+ * halved (host pool, peer-resident) or doubled (VRAM pool, not peer-resident); a late layer's
+ * counts decay every 512 (VRAM) or 128 (host) ticks. switch_target_layer turns layer < 40 late
+ * once; a VRAM pool unpins that layer's placement pins and adds one budget slot per pin.
+ * fast_minima is accepted for the interface: victims are always the full-scan minimum, which is
+ * the reference's cached choice too. ds41_pool_late: 1 if the layer is late. */
+int ds41_pool_peer(void *pool, void *peer, int host);
+int ds41_pool_exclusive(void *pool, int enabled);
+int ds41_pool_decay_interval(void *pool, uint32_t interval);
+int ds41_pool_fast_minima(void *pool, int enabled);
+int ds41_pool_switch_target_layer(void *pool, const ds41_placement *placement, int layer);
+int ds41_pool_late(void *pool, int layer);
+/* DriftPolicy (store.hpp:161-178, store.cpp:220-255): a width-one token-major controller over a
+ * VRAM pool and its RAM pool (it peers them). Each target layer's demand of a token is bracketed
+ * by ds41_drift_before / ds41_drift_after in layer order 0..39; after 128 complete tokens whose
+ * VRAM-pin hit rate is below one half, the next token's layer 0 turns every target layer of both
+ * pools late. The placement must be soft, distinct, recent 2, decay 256. Errors as the pool's. */
+int ds41_drift_create(const ds41_placement *placement, void *vram_pool, void *ram_pool, void **drift,
+                      char *error, size_t error_bytes);
+int ds41_drift_before(void *drift, const uint32_t *ids, int n);
+int ds41_drift_after(void *drift, const uint32_t *ids, int n);
+int ds41_drift_active(void *drift);                                   /* 1, 0 */
+uint64_t ds41_drift_completed_tokens(void *drift);
+const char *ds41_drift_error(void *drift);
+int ds41_drift_destroy(void *drift);
 
 /* Dynamic HBM cache for the stack's host-tier experts, the reference's VRAM slot pool in front
  * of its host tier (components/moe/src/offload.cpp:240-381 load, SlotPool policy store.cpp).

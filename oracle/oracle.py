@@ -139,6 +139,25 @@ def refpool():
             getattr(R, f).argtypes = [ctypes.c_void_p, ctypes.c_uint32]
         R.refplacement_load.argtypes = [ctypes.c_char_p, P, P, P, P, P, ctypes.c_int, P, P, ctypes.c_int]
         R.refrecords_load.argtypes = [ctypes.c_char_p, ctypes.c_int, P, ctypes.c_int, P, P, P]
+        R.refpool_retain.restype = ctypes.c_void_p
+        R.refpool_retain.argtypes = [ctypes.c_void_p, ctypes.c_uint32, P]
+        R.refpool_token_release.argtypes = [ctypes.c_void_p]
+        R.refpool_reserve.argtypes = [ctypes.c_void_p, ctypes.c_size_t, P, ctypes.c_int, P]
+        R.refpool_drained.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+        R.refpool_peer.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+        for f in ("refpool_exclusive", "refpool_fast_minima"):
+            getattr(R, f).argtypes = [ctypes.c_void_p, ctypes.c_int]
+        R.refpool_decay_interval.argtypes = [ctypes.c_void_p, ctypes.c_uint]
+        R.refpool_switch_target_layer.argtypes = [ctypes.c_void_p, P, ctypes.c_int, ctypes.c_uint]
+        R.refdrift_create.restype = ctypes.c_void_p
+        R.refdrift_create.argtypes = [P, ctypes.c_int, ctypes.c_uint, ctypes.c_uint, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p, ctypes.c_void_p, P]
+        R.refdrift_before.argtypes = [ctypes.c_void_p, P, ctypes.c_int]
+        R.refdrift_after.argtypes = [ctypes.c_void_p, P, ctypes.c_int]
+        R.refdrift_active.argtypes = [ctypes.c_void_p]
+        R.refdrift_tokens.argtypes = [ctypes.c_void_p]
+        R.refdrift_tokens.restype = ctypes.c_uint64
+        R.refdrift_destroy.argtypes = [ctypes.c_void_p]
         _refpool = R
     return _refpool
 

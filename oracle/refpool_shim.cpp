@@ -8,6 +8,7 @@
 #include <cstring>
 #include <fstream>
 #include <stdexcept>
+#include <unordered_set>
 #include <vector>
 #include "ds41/store.hpp"
 
@@ -151,4 +152,80 @@ int refrecords_load(const char *path, int cap, uint64_t *rec, int ecap, uint64_t
     return (int)r.size();
   });
 }
+// Two-tier extensions of the reference SlotPool and its drift controller.
+void *refpool_retain(void *p, uint32_t id, int *rc) {
+  void *out = nullptr;
+  *rc = guarded([&] {
+    out = new std::shared_ptr<const void>(static_cast<ds41::SlotPool *>(p)->retain(id));
+    return 0;
+  });
+  return out;
+}
+void refpool_token_release(void *t) { delete static_cast<std::shared_ptr<const void> *>(t); }
+int refpool_reserve(void *p, size_t target, const uint32_t *wanted, int n, int64_t *out) {
+  return guarded([&] {
+    std::unordered_set<ds41::ExpertId> w(wanted, wanted + n);
+    return put(static_cast<ds41::SlotPool *>(p)->reserve(target, w), out);
+  });
+}
+int refpool_drained(void *p, size_t slot) {
+  return guarded([&] {
+    static_cast<ds41::SlotPool *>(p)->drained(slot);
+    return 0;
+  });
+}
+int refpool_peer(void *p, void *peer, int host) {
+  static_cast<ds41::SlotPool *>(p)->peer(static_cast<const ds41::SlotPool *>(peer), host != 0);
+  return 0;
+}
+int refpool_exclusive(void *p, int on) {
+  static_cast<ds41::SlotPool *>(p)->exclusive(on != 0);
+  return 0;
+}
+int refpool_decay_interval(void *p, unsigned d) {
+  static_cast<ds41::SlotPool *>(p)->decay_interval(d);
+  return 0;
+}
+int refpool_fast_minima(void *p, int on) {
+  static_cast<ds41::SlotPool *>(p)->fast_minima(on != 0);
+  return 0;
+}
+int refpool_switch_target_layer(void *p, const uint32_t *pins, int npins, unsigned layer) {
+  return guarded([&] {
+    ds41::Placement q;
+    q.vram_pins.assign(pins, pins + npins);
+    static_cast<ds41::SlotPool *>(p)->switch_target_layer(q, layer);
+    return 0;
+  });
+}
+void *refdrift_create(const uint32_t *pins, int npins, unsigned recent, unsigned decay, int distinct, int hard,
+                      void *vram, void *ram, int *rc) {
+  void *out = nullptr;
+  *rc = guarded([&] {
+    ds41::Placement q;
+    q.vram_pins.assign(pins, pins + npins);
+    q.recent_window = recent;
+    q.decay_interval = decay;
+    q.distinct_lfu = distinct != 0;
+    q.hard_layer_budgets = hard != 0;
+    out = new ds41::DriftPolicy(q, *static_cast<ds41::SlotPool *>(vram), *static_cast<ds41::SlotPool *>(ram));
+    return 0;
+  });
+  return out;
+}
+int refdrift_before(void *d, const uint32_t *ids, int n) {
+  return guarded([&] {
+    static_cast<ds41::DriftPolicy *>(d)->before(std::vector<ds41::ExpertId>(ids, ids + n));
+    return 0;
+  });
+}
+int refdrift_after(void *d, const uint32_t *ids, int n) {
+  return guarded([&] {
+    static_cast<ds41::DriftPolicy *>(d)->after(std::vector<ds41::ExpertId>(ids, ids + n));
+    return 0;
+  });
+}
+int refdrift_active(void *d) { return static_cast<ds41::DriftPolicy *>(d)->active() ? 1 : 0; }
+uint64_t refdrift_tokens(void *d) { return static_cast<ds41::DriftPolicy *>(d)->completed_tokens(); }
+void refdrift_destroy(void *d) { delete static_cast<ds41::DriftPolicy *>(d); }
 }
