@@ -692,6 +692,7 @@ def bench_fp8_shared(gpu, x_pool, wg, bias, table, steps, warmup, T=4, H=4096, I
     args = [G.make_layer_args(x_pool[i], wg, bias, table, 0, -1, T, H, I, E, K, y, ws) for i in range(pool)]
     for a in args:
         a.shared_fp8 = ctypes.addressof(f8)
+        a.weight_layout = LAYOUT["weights"]  # the routed experts are configs[1]'s table, in its layout
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         G.moe_layer(args[i % pool], stream)
