@@ -225,3 +225,25 @@ def test_accept_top_p_distinct_logits_equal_p(gpu):
     assert got == want
     assert set(t[0] for t in got) == {0, 1, 2}
     assert fallbacks == len(got)  # the near-tie check sends every step down the exact path
+
+
+def test_accept_top_p_crossing_bin_beyond_lds_list(gpu):
+    """Logits within one coarse bin (x in [1, 1.25): the first digit of the key cannot separate them)
+    over 20,000 elements: the crossing bin holds far more than the 6,144 elements the finish kernel
+    lists in LDS, so its later passes histogram the whole row instead. Draws must still be the
+    host's."""
+    rng = np.random.default_rng(31)
+    x = (1.0 + rng.random((1, 20000)) * 0.2499).astype(np.float32)
+    got, want, _ = bonus_draws(gpu, x, 1.0, 0.4, 24)
+    assert got == want
+
+
+def test_accept_top_p_vocabulary_rows_listed_path(gpu):
+    """Vocabulary-sized rows (V = 129,280, logits N(0, 2.5^2)): the crossing bin of the first pass
+    holds a few hundred elements, listed in LDS for the later passes; draws are the host's at
+    top-p 0.95, 0.9 and 0.5."""
+    rng = np.random.default_rng(32)
+    x = (rng.standard_normal((1, 129280)) * 2.5).astype(np.float32)
+    for top_p in (0.95, 0.9, 0.5):
+        got, want, _ = bonus_draws(gpu, x, 1.0, top_p, 6)
+        assert got == want, top_p
