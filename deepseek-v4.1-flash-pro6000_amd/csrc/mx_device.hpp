@@ -410,13 +410,13 @@ struct Gemv16 {
   // xt: activation rows in LDS; lsw: this lane's weight-scale row in LDS (ng bytes).
   // Chunks past the end read the zero chunk of the activation rows (exact zero
   // products against a finite weight scale), so no MFMA sits behind a branch.
+  // acc: the sum so far (a chain's carry), continued chunk by chunk in k order.
   template <bool Split = false>
-  __device__ __forceinline__ v4f run(const XTile &xt, const uint8_t *lsw) {
+  __device__ __forceinline__ v4f run(const XTile &xt, const uint8_t *lsw, v4f acc = v4f{0.f, 0.f, 0.f, 0.f}) {
     const int lane = threadIdx.x & 63, q = lane >> 4, i = lane & 15;
     const SplitLane sl = split_lane(i, xt.tokens, Split);  // padded rows repeat row 0; outputs dropped
     const uint8_t *xa = xt.q + sl.src * xt.stride + 16 * q;
     const uint8_t *sa = xt.s + sl.src * xt.sstride + q;
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
     auto mma = [&](const uint4 &wv, int c, int sw) {
       const int cx = c < nch ? c : nch;  // nch is the zero chunk
       uint4 lo = *reinterpret_cast<const uint4 *>(xa + 128 * cx);
