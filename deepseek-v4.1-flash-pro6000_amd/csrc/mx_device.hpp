@@ -75,6 +75,11 @@ __device__ __forceinline__ uint32_t mxfp8_exponent(float amax) {
   return (b >> 23) + ((b & 0x7fffffu) != 0u);
 }
 
+// E4M3 code of v in a 32-group whose MXFP8 scale exponent is e (mxfp4.cu:16-19 scaling).
+__device__ __forceinline__ uint8_t mx8_code(float v, uint32_t e) {
+  return (uint8_t)e4m3_from_f32(fminf(448.f, fmaxf(-448.f, v / __uint_as_float(e << 23))));
+}
+
 // Bounded acquire-wait on a residency flag (mxfp4.cu:36-43 semantics): relaxed
 // device-coherent polls, then one acquire fence once the expected generation is
 // seen. Gives up after kReadyWaitTicks of the 100 MHz constant wall clock
