@@ -36,7 +36,7 @@ PEAK_FP4_TFLOPS = 10100.0
 # HBM bytes per gate/up/act launch (tiled weights) from rocprofv3 FETCH_SIZE (x2.0) + WRITE_SIZE (x1.0),
 # calibrated on a plain 1 GiB device copy, at mean U = 23.328 routed experts + shared
 # (profiles/verify_layer_config1_traffic.md); the algorithmic figure at that U is 304,923,000 B.
-GATE_UP_TRAFFIC_BYTES = 305_493_000
+GATE_UP_TRAFFIC_BYTES = 305_567_000
 METRIC = "verify tokens/s per MTP step (T=1+k); MoE HBM GB/s as % of 8 TB/s peak"
 # Expert weight layout of the configs[1] and configs[4] legs: 1 = tiled (ds41_expert_slab_tile, the MFMA
 # operand order), 0 = the checkpoint's row-major layout. The synthetic weights are uniform random bytes,
