@@ -588,14 +588,18 @@ def bench_drafter(gpu, steps, warmup, seed=6):
     import ds41_gfx950 as G
     H, I, E, R = 5120, 2304, 3 * 128, 5
     g = torch.Generator(device=gpu).manual_seed(seed)
-
-    def rnd(shape, lo, hi):
-        return torch.randint(lo, hi, shape, dtype=torch.uint8, device=gpu, generator=g)
-
-    P = dict(gate=rnd((E, I, H // 2), 0, 256), gate_scale=rnd((E, I, H // 32), 119, 124),
-             up=rnd((E, I, H // 2), 0, 256), up_scale=rnd((E, I, H // 32), 119, 124),
-             down=rnd((E, H, I // 2), 0, 256), down_scale=rnd((E, H, I // 32), 119, 124))
-    table, _ = G.device_table([{k: v[e] for k, v in P.items()} for e in range(E)], gpu)
+    # canonical slabs (e2m1 bytes uniform, e8m0 scales uniform over 2^-8..2^-4), tiled like the stack's
+    off, slab = G.slab_layout(H, I)
+    slabs = torch.randint(0, 256, (E, slab), dtype=torch.uint8, device=gpu, generator=g)
+    for o, m in ((off[1], I * H // 32), (off[3], I * H // 32), (off[5], H * I // 32)):
+        slabs[:, o:o + m].random_(119, 124, generator=g)
+    if LAYOUT["weights"]:
+        tiled = torch.empty_like(slabs)
+        G.slab_tile(slabs, tiled, H, I, E)
+        del slabs
+        slabs = tiled
+    entries = [G.slab_entry(slabs[e].data_ptr(), off, e) for e in range(E)]
+    table = torch.frombuffer(bytearray(b"".join(bytes(x) for x in entries)), dtype=torch.uint8).to(gpu)
     pool = 64
     scores = torch.rand((pool, R, 128), generator=g, device=gpu)
     ids = torch.stack([G.spark_topk3(scores[i]) for i in range(pool)])
@@ -603,7 +607,7 @@ def bench_drafter(gpu, steps, warmup, seed=6):
     x = torch.randn((pool, R, H), generator=g, device=gpu).to(torch.bfloat16)
     out = torch.empty((R, 3, H), dtype=torch.bfloat16, device=gpu)
     stream = torch.cuda.current_stream()
-    svc = G.TargetExperts(table, 0, H, I, stream=stream)
+    svc = G.TargetExperts(table, 0, H, I, stream=stream, weight_layout=LAYOUT["weights"])
     for i in range(warmup):
         svc(i % 3, x[i % pool], ids[i % pool], w[i % pool], out)
     torch.cuda.synchronize()
@@ -623,7 +627,7 @@ def bench_drafter(gpu, steps, warmup, seed=6):
     names = ["quant", "plan", "gate_up_act", "down"]
     NS = 2 * len(names)
     st = G.Events(NS)
-    svc_t = G.TargetExperts(table, 0, H, I, stream=stream, events=st.ptr(0))
+    svc_t = G.TargetExperts(table, 0, H, I, stream=stream, events=st.ptr(0), weight_layout=LAYOUT["weights"])
     ktot = {n: 0.0 for n in names}
     for i in range(steps):  # the handle's one event set is read back after every call
         svc_t(i % 3, x[i % pool], ids[i % pool], w[i % pool], out)
@@ -640,13 +644,14 @@ def bench_drafter(gpu, steps, warmup, seed=6):
     gu_bytes = 2 * (I * H // 2 + I * H // 32)
     res = {"workload": "MTP drafter routed experts: 5 rows, hidden 5120, 3 stages x 128 experts (I=2304, MXFP4) "
                        "top-3 (drafter router top-3 over random scores), route weights random",
+           "weight_layout": "tiled" if LAYOUT["weights"] else "row-major",
            "steps": steps, "us_per_call": us, "mean_unique_experts": U,
            "hbm_gbps": U * ebytes / (us * 1e-6) / 1e9, "hbm_frac": U * ebytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
            "kernel_us": ktot, "gate_up_gbps": U * gu_bytes / (ktot["gate_up_act"] * 1e-6) / 1e9,
            "top3_us_per_call": top3_us}
     log(f"drafter experts: {us:.1f} us/call, U={U:.2f}, HBM {res['hbm_gbps']:.0f} GB/s; kernels " +
         ", ".join(f"{n} {ktot[n]:.1f}" for n in names) + f"; top-3 {top3_us:.1f} us")
-    del P, table
+    del slabs, table
     torch.cuda.empty_cache()
     return res
 

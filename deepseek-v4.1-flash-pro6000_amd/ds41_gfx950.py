@@ -909,7 +909,7 @@ class Records:
 class TargetExpertsDesc(ctypes.Structure):
     _fields_ = [("table", ctypes.c_void_p), ("expert_base", ctypes.c_int32), ("hidden", ctypes.c_int32),
                 ("inter", ctypes.c_int32), ("swiglu_limit", ctypes.c_float), ("check_routes", ctypes.c_int32),
-                ("stream", ctypes.c_void_p), ("stage_events", ctypes.c_void_p)]
+                ("stream", ctypes.c_void_p), ("stage_events", ctypes.c_void_p), ("weight_layout", ctypes.c_int32)]
 
 
 class TargetExperts:
@@ -918,10 +918,11 @@ class TargetExperts:
     the stream given here. call() raises with the library's error text on failure."""
 
     def __init__(self, table, expert_base, hidden, inter, swiglu_limit=10.0, check_routes=False, stream=None,
-                 events=None):
+                 events=None, weight_layout=0):
         self.stream = _stream(stream)
         self.desc = TargetExpertsDesc(table.data_ptr(), expert_base, hidden, inter, swiglu_limit,
-                                      1 if check_routes else 0, self.stream, 0 if events is None else events)
+                                      1 if check_routes else 0, self.stream, 0 if events is None else events,
+                                      weight_layout)
         self.handle = ctypes.c_void_p(0)
         check(lib().ds41_target_experts_create(ctypes.byref(self.desc), ctypes.byref(self.handle)),
               "ds41_target_experts_create")

@@ -538,6 +538,9 @@ typedef struct ds41_target_experts_desc {
   void *stream;                    /* every call must pass this stream (forward.cu:1003) */
   void *const *stage_events;       /* optional: 8 hipEvent_t, start/stop of the quantise,
                                       plan, gate/up/act and down kernels */
+  int32_t weight_layout;           /* 0: the reference's row-major tensors; 1: every entry points
+                                      into slabs tiled by ds41_expert_slab_tile (same outputs,
+                                      contiguous weight loads). Not in the reference's struct. */
 } ds41_target_experts_desc;
 /* Allocates the workspace (8 rows x top-3) and, with check_routes, a pinned id buffer. */
 int ds41_target_experts_create(const ds41_target_experts_desc *desc, void **user);

@@ -78,12 +78,15 @@ def test_target_experts_abi_host_checks():
     import sys
     sys.path.insert(0, os.path.join(ROOT, "deepseek-v4.1-flash-pro6000_amd"))
     import ds41_gfx950 as G
-    assert ctypes.sizeof(G.TargetExpertsDesc) == 48
+    assert ctypes.sizeof(G.TargetExpertsDesc) == 56
+    assert G.TargetExpertsDesc.weight_layout.offset == 48
     lib = ctypes.CDLL(LIB)
     h = ctypes.c_void_p(0)
-    d = G.TargetExpertsDesc(0, 0, 5120, 2304, 10.0, 0, None, None)  # null table
+    d = G.TargetExpertsDesc(0, 0, 5120, 2304, 10.0, 0, None, None, 0)  # null table
     assert lib.ds41_target_experts_create(ctypes.byref(d), ctypes.byref(h)) == 1 and not h.value
-    d = G.TargetExpertsDesc(64, 0, 5000, 2304, 10.0, 0, None, None)  # hidden not a multiple of 256
+    d = G.TargetExpertsDesc(64, 0, 5000, 2304, 10.0, 0, None, None, 0)  # hidden not a multiple of 256
+    assert lib.ds41_target_experts_create(ctypes.byref(d), ctypes.byref(h)) == 1 and not h.value
+    d = G.TargetExpertsDesc(64, 0, 5120, 2304, 10.0, 0, None, None, 2)  # no such weight layout
     assert lib.ds41_target_experts_create(ctypes.byref(d), ctypes.byref(h)) == 1 and not h.value
     lib.ds41_target_experts_error.restype = ctypes.c_char_p
     assert lib.ds41_target_experts_error(None) == b"null target experts handle"

@@ -224,3 +224,48 @@ def test_spark_topk3_vs_oracle(gpu, name):
         got = host(G.spark_topk3(dev(sub, gpu)))
         want = O.spark_topk3(sub)
         assert np.array_equal(got, want), (name, m, got.tolist(), want.tolist())
+
+
+def tiled_drafter_table(gpu):
+    """The same DISTINCT experts as drafter_table, as canonical slabs tiled by ds41_expert_slab_tile,
+    behind the same 3 x 128 entries."""
+    if "tiled" in _cache:
+        return _cache["tiled"]
+    import torch
+    import ds41_gfx950 as G
+    _, _, P = drafter_table(gpu)
+    off, slab = G.slab_layout(H, I)
+    src = torch.zeros((DISTINCT, slab), dtype=torch.uint8, device=gpu)
+    for d in range(DISTINCT):
+        for name, o in zip(("gate", "gate_scale", "up", "up_scale", "down", "down_scale"), off):
+            t = P[name][d].reshape(-1)
+            src[d, o:o + t.numel()] = t
+    dst = torch.empty_like(src)
+    G.slab_tile(src, dst, H, I, DISTINCT)
+    entries = [G.DeviceExpert() for _ in range(16)] + [G.slab_entry(dst[phys(s, e)].data_ptr(), off)
+                                                      for s in range(3) for e in range(NE)]
+    table = torch.frombuffer(bytearray(b"".join(bytes(e) for e in entries)), dtype=torch.uint8).to(gpu)
+    _cache["tiled"] = (table, src, dst)
+    return _cache["tiled"]
+
+
+@pytest.mark.parametrize("rows,stage", [(1, 2), (5, 0), (8, 1)])
+def test_target_experts_tiled_weights_bitexact(gpu, rows, stage):
+    """weight_layout = 1 over tiled slabs gives the row-major service's output bit for bit."""
+    import ds41_gfx950 as G
+    table, _, _ = drafter_table(gpu)
+    ttable, _, _ = tiled_drafter_table(gpu)
+    say(f"target experts tiled vs row-major rows={rows} stage={stage}")
+    rng = np.random.default_rng(300 + 10 * rows + stage)
+    x_np = O.bf16_bits(rng.standard_normal((rows, H)).astype(np.float32))
+    ids_np = np.stack([rng.choice(NE, 3, replace=False) for _ in range(rows)]).astype(np.int32)
+    w_np = rng.uniform(0.05, 1.2, (rows, 3)).astype(np.float32)
+    svc = G.TargetExperts(table, 16, H, I)
+    tsvc = G.TargetExperts(ttable, 16, H, I, weight_layout=1)
+    want = run_case(gpu, svc, stage, x_np, ids_np, w_np)
+    got = run_case(gpu, tsvc, stage, x_np, ids_np, w_np)
+    assert G.take_status() == 0
+    assert not np.any(np.isnan(O.bf16_to_f32(got)))
+    assert np.array_equal(got, want)
+    svc.close()
+    tsvc.close()
