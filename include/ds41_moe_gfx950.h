@@ -536,8 +536,9 @@ typedef struct ds41_target_experts_desc {
                                       rejected call writes NaN to every output slot and sets
                                       status bit 4 (ds41_take_status), without a host wait. */
   void *stream;                    /* every call must pass this stream (forward.cu:1003) */
-  void *const *stage_events;       /* optional: 8 hipEvent_t, start/stop of the quantise,
-                                      plan, gate/up/act and down kernels */
+  void *const *stage_events;       /* optional: 8 hipEvent_t, start/stop of the launch that
+                                      quantises x and plans (one kernel), of nothing (the second
+                                      pair is recorded back to back), of gate/up/act and of down */
   int32_t weight_layout;           /* 0: the reference's row-major tensors; 1: every entry points
                                       into slabs tiled by ds41_expert_slab_tile (same outputs,
                                       contiguous weight loads). Not in the reference's struct. */
