@@ -128,6 +128,26 @@ def test_stack_host_tier_bitexact_vs_resident_router(gpu):
     assert s["h2d_bytes"] - before["h2d_bytes"] == fetched * st.slab and s["invalid_layers"] == 0
 
 
+@pytest.mark.parametrize("T", [1, 4, 8])
+def test_stack_route_ids_reproduce_router_routes(gpu, T):
+    """Given the route ids its router chose, a step plans beside the router and forms the route
+    weights in the gate/up epilogue (the shared expert an ordinary gate/up job), not in a plan
+    launch after the router: outputs, ids and weights must be bit-identical to the router-routed
+    step, with and without the host tier. T = 8 plans two tokens per wave."""
+    import torch
+    import ds41_gfx950 as G
+    L, H, I, E, K = 3, 1024, 256, 32, 6
+    say(f"stack route ids = router routes L={L} H={H} I={I} E={E} T={T}")
+    st = Stack(gpu, 31, L, H, I, E, K, 8, [range(3 * l, 3 * l + 8) for l in range(L)])
+    x = rand_x(gpu, 12 + T, T, H)
+    G.take_status()
+    routed = st.run("all", x)
+    rid = torch.from_numpy(np.ascontiguousarray(routed[2])).to(gpu)
+    check_same(st.run("all", x, rid), routed)
+    check_same(st.run("tier", x, rid), routed)
+    assert G.take_status() == 0
+
+
 def test_stack_layers_vs_oracle(gpu):
     L, H, I, E, K, T = 3, 512, 256, 32, 6, 4
     say(f"stack vs oracle L={L} H={H} I={I} E={E} T={T}")
@@ -194,8 +214,10 @@ def test_stack_invalid_route_ids_give_nan(gpu):
     x = rand_x(gpu, 10, T, H)
     G.take_status()
     before = st.tier.stats()
-    y, lo, _, _ = st.run("tier", x, torch.from_numpy(rid).to(gpu))
+    y, lo, _, w = st.run("tier", x, torch.from_numpy(rid).to(gpu))
     assert np.all(np.isnan(O.bf16_to_f32(lo[0])))
+    # the rejected layer's weights are still each token's normalised scores times the route scale
+    assert np.allclose(w[0].sum(axis=-1), 1.5, rtol=1e-5) and np.all(w[0] > 0)
     assert G.take_status() & 4
     assert st.tier.stats()["invalid_layers"] - before["invalid_layers"] == 1
     ok = st.run("tier", x)  # the stack recovers on the next step
