@@ -122,10 +122,13 @@ struct XTile {
 __device__ __host__ __forceinline__ int xtile_stride(int k) { return ((k + 127) / 128 + 1) * 128 + 16; }
 __device__ __host__ __forceinline__ int xtile_sstride(int k) { return (((k + 127) / 128 + 1) * 4 + 15) & ~15; }
 
-// Byte mask (0xff per byte) of the E4M3 bytes whose exponent field is >= 7 (|v| >= 1).
+// Byte mask (0xff per byte) of the E4M3 bytes with |v| >= 1 (exponent field >= 7):
+// (b & 0x78) + 0x48 has bit 7 set exactly when the exponent field is >= 7 (no
+// carry leaves the byte), and v_perm's selectors 8..11 replicate bit 7 of
+// bytes 1, 3, 5, 7 of its 8-byte operand {t, t << 8}, i.e. of t's bytes 0, 2, 1, 3.
 __device__ __forceinline__ uint32_t e4m3_big_mask(uint32_t v) {
-  const uint32_t t = (((v >> 3) & 0x0f0f0f0fu) + 0x09090909u) & 0x10101010u;
-  return (t >> 4) * 0xffu;
+  const uint32_t t = (v & 0x78787878u) + 0x48484848u;
+  return __builtin_amdgcn_perm(t, t << 8, 0x0B090A08u);
 }
 
 // Magnitude split of the activation rows. The scaled MFMA forms each K32 block
@@ -142,27 +145,28 @@ __device__ __forceinline__ uint32_t e4m3_big_mask(uint32_t v) {
 // split costs no LDS either.
 __device__ __host__ __forceinline__ int split_rows(int tokens) { return 2 * ((tokens + 3) & ~3); }
 // MFMA row i (= lane & 15) of a split XTile: source row, and the mask flip
-// (0: |v| >= 1 bytes, ~0: |v| < 1 bytes) and keep (0 for rows past 2*T4).
+// (0: |v| >= 1 bytes, ~0: |v| < 1 bytes). Rows past 2*T4 read a finite row and
+// their outputs are dropped (an MFMA output row depends on its own A row only).
 struct SplitLane {
   int src;
-  uint32_t flip, keep;
+  uint32_t flip;
 };
 __device__ __forceinline__ SplitLane split_lane(int i, int tokens, bool split) {
   const int T4 = (tokens + 3) & ~3;
-  SplitLane r{i, 0u, 0xffffffffu};
+  SplitLane r{i, 0u};
   if (split) {
     r.src = i < T4 ? i : i - T4;
     r.flip = i < T4 ? 0u : 0xffffffffu;
-    r.keep = i < 2 * T4 ? 0xffffffffu : 0u;
   }
   if (r.src >= tokens) r.src = 0;  // padding rows: any finite row, outputs dropped
   return r;
 }
+// The split half of 16 activation bytes: 6 vector operations per dword (the v_perm mask).
 __device__ __forceinline__ uint4 split_bytes(uint4 v, const SplitLane &l) {
-  v.x &= (e4m3_big_mask(v.x) ^ l.flip) & l.keep;
-  v.y &= (e4m3_big_mask(v.y) ^ l.flip) & l.keep;
-  v.z &= (e4m3_big_mask(v.z) ^ l.flip) & l.keep;
-  v.w &= (e4m3_big_mask(v.w) ^ l.flip) & l.keep;
+  v.x &= e4m3_big_mask(v.x) ^ l.flip;
+  v.y &= e4m3_big_mask(v.y) ^ l.flip;
+  v.z &= e4m3_big_mask(v.z) ^ l.flip;
+  v.w &= e4m3_big_mask(v.w) ^ l.flip;
   return v;
 }
 __device__ __forceinline__ v4f split_combine(v4f acc, int tokens) {
@@ -269,7 +273,7 @@ __device__ __forceinline__ int stage_xtile_presplit(uint8_t *lq, uint8_t *ls, co
       const int p = p0 + j * (int)blockDim.x;
       if (p >= nsrc) break;
       const int t = p / kp, off = (p - t * kp) << 4;
-      const SplitLane big{t, 0u, 0xffffffffu}, small{t, 0xffffffffu, 0xffffffffu};
+      const SplitLane big{t, 0u}, small{t, 0xffffffffu};
       *reinterpret_cast<uint4 *>(lq + t * stride + off) = split_bytes(v[j], big);
       *reinterpret_cast<uint4 *>(lq + (T4 + t) * stride + off) = split_bytes(v[j], small);
     }
