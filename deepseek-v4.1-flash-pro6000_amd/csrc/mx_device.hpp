@@ -238,6 +238,84 @@ __device__ __forceinline__ int stage_xtile(uint8_t *lq, uint8_t *ls, const uint8
   return tokens;
 }
 
+// stage_xtile of rows 0..tokens-1 of x in one memory round trip, for a big
+// workgroup whose tile is a few pieces per thread: issue() loads each thread's
+// up to NP 16-byte pieces and NS scale bytes (addresses clamped into the tile,
+// so every load is unconditional), hold() waits for all of them once, and
+// store() writes them and the trailing zero chunks to LDS. The caller may issue
+// loads of its own between issue() and hold(). A tile of more than NP * blockDim
+// pieces or NS * blockDim scale bytes, or an x not 16-byte aligned, is not
+// loaded (ok false) and store() stages it with stage_xtile. Caller syncs.
+// Quotient by a divisor 2 <= d < 2^16 fixed for the launch, as one multiply-high:
+// m = ceil(2^32 / d) gives floor(p / d) exactly for 0 <= p < 2^32 / d (the
+// rounding error of m is below 1 / d per unit of p).
+struct UDiv {
+  uint32_t d, m;
+  __device__ __forceinline__ explicit UDiv(uint32_t dd) : d(dd), m(0xffffffffu / dd + 1u) {}
+  __device__ __forceinline__ uint32_t q(uint32_t p) const { return __umulhi(p, m); }
+};
+
+template <int NP, int NS>
+struct XTileRound {
+  uint4 v[NP];
+  uint32_t b[NS];
+  bool ok;
+  __device__ __forceinline__ void issue(const uint8_t *x, const uint8_t *xs, int k, int tokens) {
+    const int kp = k >> 4, nsrc = tokens * kp, ng = k >> 5, sstride = xtile_sstride(k), bd = (int)blockDim.x;
+    ok = (((uintptr_t)x) & 15u) == 0 && tokens > 0 && nsrc <= NP * bd && tokens * sstride <= NS * bd &&
+         k < (1 << 20);
+    // Loaded whatever ok says (a branch or a value select here makes the compiler wait on each
+    // load); the clamped addresses stay inside rows 0..max(tokens, 1)-1.
+    const UDiv dkp((uint32_t)kp), dss((uint32_t)sstride);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int q = (int)threadIdx.x + j * bd, p = q < nsrc ? q : (nsrc > 0 ? nsrc - 1 : 0);
+      const int t = (int)dkp.q((uint32_t)p), off = (p - t * kp) << 4;
+      const u32x4 u = *(global_u4u)(x + (size_t)t * k + off);
+      v[j] = make_uint4(u.x, u.y, u.z, u.w);
+    }
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int p = (int)threadIdx.x + j * bd, t = (int)dss.q((uint32_t)p), g = p - t * sstride;
+      const int tc = t < tokens ? t : (tokens > 0 ? tokens - 1 : 0), gc = g < ng ? g : ng - 1;
+      b[j] = xs[(size_t)tc * ng + gc];
+    }
+  }
+  __device__ __forceinline__ void hold() {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) asm volatile("" : "+v"(v[j].x), "+v"(v[j].y), "+v"(v[j].z), "+v"(v[j].w));
+#pragma unroll
+    for (int j = 0; j < NS; ++j) asm volatile("" : "+v"(b[j]));
+  }
+  __device__ __forceinline__ void store(uint8_t *lq, uint8_t *ls, const uint8_t *x, const uint8_t *xs, int k,
+                                        int tokens) const {
+    if (!ok) {
+      stage_xtile(lq, ls, x, xs, k, tokens, [](int r) { return (size_t)r; });
+      return;
+    }
+    const int stride = xtile_stride(k), sstride = xtile_sstride(k), pieces = (stride - 16) >> 4;
+    const int kp = k >> 4, nsrc = tokens * kp, ng = k >> 5, bd = (int)blockDim.x;
+    const UDiv dkp((uint32_t)kp), dss((uint32_t)sstride);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int p = (int)threadIdx.x + j * bd;
+      if (p >= nsrc) break;
+      const int t = (int)dkp.q((uint32_t)p), off = (p - t * kp) << 4;
+      *reinterpret_cast<uint4 *>(lq + t * stride + off) = v[j];
+    }
+    for (int p = threadIdx.x; p < tokens * (pieces - kp); p += bd) {  // trailing zeros
+      const int r = p / (pieces - kp), pc = kp + (p - r * (pieces - kp));
+      *reinterpret_cast<uint4 *>(lq + r * stride + (pc << 4)) = make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int p = (int)threadIdx.x + j * bd;
+      if (p >= tokens * sstride) break;
+      ls[p] = p - (int)dss.q((uint32_t)p) * sstride < ng ? (uint8_t)b[j] : (uint8_t)127;
+    }
+  }
+};
+
 // Pre-split staging: split_rows(tokens) LDS rows, row t = the |v| >= 1 bytes of
 // source row t and row T4 + t its |v| < 1 bytes (padding rows zero, scales
 // 127), read by a GEMV with XTile.split = 0. It costs twice the LDS of
