@@ -67,6 +67,21 @@ __device__ __forceinline__ uint32_t e4m3_from_f32(float v) {
   return sign | (uint32_t)(((e + 7) << 3) | (int)r);
 }
 
+// E4M3 code of v clamped to [-448, 448] (fminf / fmaxf return the number, so a NaN v gives the
+// code of -448): the hardware converter, round to nearest even. On gfx950 it equals
+// e4m3_from_f32 for every fp32 in [-448, 448] (all 2^31-odd of them are compared by
+// ds41_e4m3_converter_check), so the quantisers keep the integer formulation's bits.
+__device__ __forceinline__ float e4m3_clamp(float v) { return fminf(448.f, fmaxf(-448.f, v)); }
+__device__ __forceinline__ uint32_t e4m3_sat(float v) {
+  const float c = e4m3_clamp(v);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, c, 0, false) & 0xffu;
+}
+// Four codes in one dword, value i in byte i.
+__device__ __forceinline__ uint32_t e4m3_sat4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(e4m3_clamp(a), e4m3_clamp(b), 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(e4m3_clamp(c), e4m3_clamp(d), lo, true);
+}
+
 // MXFP8 scale exponent of a 32-group from its amax (mxfp4.cu:16-19):
 // e = ceil-to-power-of-two exponent of fp32(max(amax, 1e-4) * (1/448)).
 __device__ __forceinline__ uint32_t mxfp8_exponent(float amax) {
@@ -77,7 +92,7 @@ __device__ __forceinline__ uint32_t mxfp8_exponent(float amax) {
 
 // E4M3 code of v in a 32-group whose MXFP8 scale exponent is e (mxfp4.cu:16-19 scaling).
 __device__ __forceinline__ uint8_t mx8_code(float v, uint32_t e) {
-  return (uint8_t)e4m3_from_f32(fminf(448.f, fmaxf(-448.f, v / __uint_as_float(e << 23))));
+  return (uint8_t)e4m3_sat(v / __uint_as_float(e << 23));
 }
 
 // Bounded acquire-wait on a residency flag (mxfp4.cu:36-43 semantics): relaxed
@@ -378,6 +393,98 @@ __device__ __forceinline__ int stage_xtile_presplit(uint8_t *lq, uint8_t *ls, co
   }
   return nrows;
 }
+// MXFP8 codes of 16 consecutive values of a 32-group whose other 16 values sit in the
+// neighbouring lane (lane ^ 1): the group's exponent from both halves' amax, then the codes of
+// mx8_code. For 1 <= e <= 253 the power-of-two divisor's reciprocal is a normal float, so the
+// product rounds exactly as the quotient does; other exponents (an infinite or NaN amax) take the
+// quotient itself.
+__device__ __forceinline__ uint4 mx8_codes16(const float *f, uint32_t *e_out) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  const uint32_t e = mxfp8_exponent(amax);
+  *e_out = e;
+  uint32_t w[4];
+  if (e - 1u <= 252u) {
+    const float inv = __uint_as_float((254u - e) << 23);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = e4m3_sat4(f[4 * i] * inv, f[4 * i + 1] * inv, f[4 * i + 2] * inv, f[4 * i + 3] * inv);
+  } else {
+    const float d = __uint_as_float(e << 23);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = e4m3_sat4(f[4 * i] / d, f[4 * i + 1] / d, f[4 * i + 2] / d, f[4 * i + 3] / d);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// stage_xtile (Presplit false) or stage_xtile_presplit (Presplit true) of `tokens` rows of the
+// bf16 matrix x [*][k], quantised to MXFP8 on the way (the codes and exponents the MXFP8
+// quantiser writes for the same rows). A thread takes one 16-value half of a 32-group per trip;
+// the group's halves are neighbouring lanes, so every lane runs every trip (loads clamped into
+// the tile, stores skipped past its end). Returns the LDS row count. Caller syncs.
+template <bool Presplit, class RowIdx>
+__device__ __forceinline__ int stage_xtile_bf16(uint8_t *lq, uint8_t *ls, const uint16_t *x, int k, int tokens,
+                                                RowIdx row_idx) {
+  const int stride = xtile_stride(k), sstride = xtile_sstride(k);
+  const int T4 = (tokens + 3) & ~3, nrows = Presplit ? 2 * T4 : tokens, srows = Presplit ? T4 : tokens;
+  const int pieces = (stride - 16) >> 4, kp = k >> 4, ng = k >> 5, bd = (int)blockDim.x;
+  const int nsrc = tokens * kp;
+  const bool aligned = (((uintptr_t)x) & 15u) == 0;
+  for (int p0 = 0; p0 < nsrc; p0 += 2 * bd) {
+    u32x4 v[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int q = p0 + (int)threadIdx.x + j * bd, p = q < nsrc ? q : nsrc - 1;
+      const int t = p / kp, pc = p - t * kp;
+      const uint16_t *src = x + (size_t)row_idx(t) * k + 16 * pc;
+      if (aligned) {
+        v[j][0] = *(global_u4)(src);
+        v[j][1] = *(global_u4)(src + 8);
+      } else {
+        v[j][0] = *(global_u4u)(src);
+        v[j][1] = *(global_u4u)(src + 8);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int q = p0 + (int)threadIdx.x + j * bd, p = q < nsrc ? q : nsrc - 1;
+      const int t = p / kp, pc = p - t * kp;
+      const uint32_t wd[8] = {v[j][0].x, v[j][0].y, v[j][0].z, v[j][0].w, v[j][1].x, v[j][1].y, v[j][1].z, v[j][1].w};
+      float f[16];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        f[2 * i] = __uint_as_float(wd[i] << 16);
+        f[2 * i + 1] = __uint_as_float(wd[i] & 0xffff0000u);
+      }
+      uint32_t e;
+      const uint4 c = mx8_codes16(f, &e);  // every lane: its neighbour needs its amax
+      if (q < nsrc) {
+        if (Presplit) {
+          const SplitLane big{t, 0u}, small{t, 0xffffffffu};
+          *reinterpret_cast<uint4 *>(lq + t * stride + 16 * pc) = split_bytes(c, big);
+          *reinterpret_cast<uint4 *>(lq + (T4 + t) * stride + 16 * pc) = split_bytes(c, small);
+        } else {
+          *reinterpret_cast<uint4 *>(lq + t * stride + 16 * pc) = c;
+        }
+        if (!(pc & 1)) {
+          ls[t * sstride + (pc >> 1)] = (uint8_t)e;
+          if (Presplit) ls[(T4 + t) * sstride + (pc >> 1)] = (uint8_t)e;
+        }
+      }
+    }
+  }
+  for (int p = threadIdx.x; p < nrows * pieces; p += bd) {  // trailing chunk, padding rows
+    const int r = p / pieces, pc = p - r * pieces, t = r < srows ? r : r - T4;
+    if (pc >= kp || t >= tokens) *reinterpret_cast<uint4 *>(lq + r * stride + (pc << 4)) = make_uint4(0, 0, 0, 0);
+  }
+  for (int p = threadIdx.x; p < nrows * sstride; p += bd) {  // scale padding, padding rows
+    const int r = p / sstride, g = p - r * sstride, t = r < srows ? r : r - T4;
+    if (g >= ng || t >= tokens) ls[p] = (uint8_t)127;
+  }
+  return nrows;
+}
+
 // The pre-split tile when it fits `budget` bytes of LDS.
 __host__ __device__ __forceinline__ bool presplit_fits(int tokens, int k, int budget) {
   return (size_t)split_rows(tokens) * (xtile_stride(k) + xtile_sstride(k)) <= (size_t)budget;

@@ -292,26 +292,33 @@ typedef struct ds41_stack_stats {
   uint64_t host_fetched;           /* host-tier experts copied in (on demand or by a prefetch) */
   uint64_t h2d_bytes;
   uint64_t invalid_layers;         /* layer passes whose routes were rejected */
-  uint64_t cached_routed;          /* routed host-tier experts the HBM cache already held at the plan */
+  uint64_t cached_routed;          /* routed host-tier experts served from the HBM cache (held when the
+                                      plan ran, or landed by a prefetch before the layer's jobs) */
 } ds41_stack_stats;
 
-/* Creates a stack (allocates: the layer workspace, max_tokens*topk staging
- * slots, two activation buffers, a pinned plan read-back buffer, a copy stream
- * at default priority and two events, on the current device). *stack receives
+/* Creates a stack (allocates: the layer workspace, per-layer plan buffers,
+ * 2*max_tokens*topk staging slots, two activation buffers, pinned plan
+ * read-back mirrors (one per layer), a copy stream at default priority and two
+ * events, on the current device). *stack receives
  * an opaque handle. The verify-step counterpart of the MoE part of the
  * reference's Forward::verify (engine/src/forward.cu:769, batched through
  * engine/src/hotpath/batch.inc:220-335), with OffloadStore::order/upload
  * (components/moe/src/offload.cpp:443-457) as the host tier. */
 int ds41_verify_stack_create(const ds41_stack_desc *desc, void **stack);
 /* One verify step of `tokens` rows (1..max_tokens) through every layer: layer l
- * takes layer l-1's output (layer 0 takes x). Per layer: router + plan on
- * `stream`; a read-back of the plan (one host wait per layer that has a host
- * tier, as the reference's per-layer route-event wait, batch.inc:224); resident gate/up and
+ * takes layer l-1's output (layer 0 takes x).
+ * Router routing (route_ids NULL), per layer: router + plan on `stream`; a
+ * read-back of the plan (one host wait per layer that has a host tier, as the
+ * reference's per-layer route-event wait, batch.inc:224); resident gate/up and
  * down run while the host issues hipMemcpyAsync of the routed host-tier slabs
- * on the copy stream into staging slots; host-tier gate/up and down wait on the
- * copies' event; then the ordered reduce.
- * route_ids: nullable device int32 [layers][tokens][topk] that replaces the
- * router's top-k (the weights still come from the router's scores).
+ * on the copy stream; host-tier gate/up and down wait on the copies' event;
+ * then the ordered reduce.
+ * Caller routing (route_ids: device int32 [layers][tokens][topk] that replaces
+ * the router's top-k; the weights still come from the router's scores): every
+ * layer is planned in one launch at the start of the step and the host reads
+ * all the plans once (one wait per step, while layer 0 runs), then issues every
+ * layer's host-tier copies and enqueues every layer without another wait; a
+ * layer is then two launches (router + gate/up/act, down + reduce).
  * layer_out (nullable, device bf16 [layers][tokens][hidden]): every layer's
  * output; ids_out / weights_out (nullable, device [layers][tokens][topk]).
  * Steps on one stack must not overlap (one workspace and staging area). */
@@ -579,6 +586,12 @@ const char *ds41_gfx950_version(void);
  * (device, blocks * 256 * 4 bytes). Timing it gives the practical HBM read
  * ceiling that the HBM-bound kernels' rates are compared against. */
 int ds41_hbm_read_probe(const void *buf, size_t bytes, void *sink, int blocks, void *stream);
+/* Self-check of the device's E4M3 converter (no counterpart in the reference): the MXFP8
+ * quantisers convert with the hardware instruction, which must round exactly as the integer
+ * formulation of OCP E4M3 (round to nearest even, saturating) on every fp32 in [-448, 448].
+ * Adds the number of disagreeing conversions to *mismatches (device, caller-zeroed) on `stream`;
+ * 0 is the only acceptable result. About 2.3e9 inputs; well under a second. */
+int ds41_e4m3_converter_check(unsigned long long *mismatches, void *stream);
 /* Reads and clears the kernels' status bits (synchronous): 1 a residency wait
  * gave up (the rows that needed those weights are written as NaN), 2 a job's
  * row count was outside 1..8, 4 invalid/duplicate routes. */

@@ -88,6 +88,21 @@ def test_quantize_mxfp8_bitexact(gpu):
     assert np.array_equal(host(s), sr) and np.array_equal(host(q), qr)
 
 
+def test_e4m3_hardware_converter_exact(gpu):
+    """The quantisers convert with the device's E4M3 instruction; it must round exactly as the
+    integer formulation of OCP E4M3 (nearest even, saturating) on every fp32 in [-448, 448],
+    every value the clamped quantisers hand it (ds41_e4m3_converter_check, ~2.3e9 inputs, both
+    byte positions of the packed form)."""
+    import ctypes
+    import torch
+    import ds41_gfx950 as G
+    say("e4m3 converter, every fp32 in [-448, 448]")
+    bad = torch.zeros(1, dtype=torch.int64, device=gpu)
+    assert G.lib().ds41_e4m3_converter_check(ctypes.c_void_p(bad.data_ptr()), None) == 0
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 0
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 512, 1024), (1, 1024, 512), (4, 2880, 4096), (4, 4096, 2880),
                                    (8, 100, 96), (3, 17, 32), (5, 64, 160), (11, 48, 256)])
 def test_raw_projection_vs_oracle(gpu, m, n, k):
