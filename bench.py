@@ -222,9 +222,15 @@ def bench_layer(gpu, steps, warmup, cpu_seconds, no_cpu, fp8_legs=True):
         f"{gate_gbps:.0f} GB/s, down {down_gbps:.0f} GB/s, layer {layer_gbps:.0f} GB/s "
         f"({layer_gbps / PEAK_HBM_GBPS * 100:.1f}% of 8 TB/s), mean unique experts {mean_u:.2f}")
 
-    ceiling = read_ceiling(gpu, stream)
-    log(f"streaming-read ceiling (ds41_hbm_read_probe, 1 GiB, 2048 WGs): {ceiling:.0f} GB/s; "
+    ceiling, ceiling_sweep = read_ceiling(gpu, stream)
+    best = max(ceiling_sweep, key=lambda r: r["gbps"])
+    log(f"streaming-read ceiling (ds41_hbm_read_probe_ex, 1 GiB, best of {len(ceiling_sweep)}: "
+        f"{best['blocks']} WGs, {best['loads_in_flight']} loads in flight, "
+        f"{'non-temporal' if best['nontemporal'] else 'plain'}): {ceiling:.0f} GB/s; "
         f"gate_up_act at {gate_gbps / ceiling * 100:.1f}% of it")
+    for r in ceiling_sweep:
+        log(f"  read probe {r['blocks']:5d} WGs x {r['loads_in_flight']:2d} loads "
+            f"{'nt   ' if r['nontemporal'] else 'plain'}: {r['gbps']:.0f} GB/s")
 
     fp8_shared = bench_fp8_shared(gpu, x_pool, wg, bias, table, steps, warmup) if fp8_legs else None
 
@@ -252,7 +258,8 @@ def bench_layer(gpu, steps, warmup, cpu_seconds, no_cpu, fp8_legs=True):
                      "traffic": GATE_UP_TRAFFIC_BYTES,
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, calibrated)",
                      "bytes_per_launch": (mean_u + 1) * GATE_UP_BYTES, "launch_us": launch_us["gate_up_act"],
-                     "measured_read_ceiling": ceiling, "frac_of_measured_ceiling": gate_gbps / ceiling},
+                     "measured_read_ceiling": ceiling, "frac_of_measured_ceiling": gate_gbps / ceiling,
+                     "read_ceiling_probe": {"best": best, "sweep": ceiling_sweep}},
         "cpu_baseline": cpu,
         "fp8_shared": fp8_shared,
     }
@@ -473,25 +480,34 @@ def bench_accept(gpu, steps, cpu_seconds, no_cpu, top_p=1.0):
             "bytes_per_step": 7 * V * 4, "cpu_baseline": cpu}
 
 
-def read_ceiling(gpu, stream, nbytes=1 << 30, blocks=2048, reps=10):
-    """GB/s of ds41_hbm_read_probe streaming nbytes once per launch (events around reps launches):
-    the practical read ceiling next to the published 8 TB/s."""
+def read_ceiling(gpu, stream, nbytes=1 << 30, reps=10):
+    """The device's streaming-read ceiling: ds41_hbm_read_probe_ex streaming nbytes (4x the 256 MB
+    last-level cache) once per launch, timed with events around reps launches, over a sweep of
+    loads in flight per thread (4, 8, 16), plain and non-temporal loads, and 1k-8k workgroups.
+    Returns (best GB/s, the sweep as a list of dicts)."""
     import torch
     import ds41_gfx950 as G
     buf = torch.ones(nbytes, dtype=torch.uint8, device=gpu)
-    sink = torch.empty(blocks * 256, dtype=torch.int32, device=gpu)
-    for _ in range(2):
-        G.hbm_read_probe(buf, sink, blocks, stream)
-    ev = G.Events(2)
-    torch.cuda.synchronize()
-    ev.record(0, stream)
-    for _ in range(reps):
-        G.hbm_read_probe(buf, sink, blocks, stream)
-    ev.record(1, stream)
-    torch.cuda.synchronize()
-    gbps = nbytes * reps / (ev.elapsed(0, 1) * 1e-3) / 1e9
-    del buf, sink
-    return gbps
+    sweep = []
+    for blocks in (1024, 2048, 4096, 8192):
+        sink = torch.empty(blocks * 256, dtype=torch.int32, device=gpu)
+        for u in (4, 8, 16):
+            for nt in (0, 1):
+                for _ in range(2):
+                    G.hbm_read_probe_ex(buf, sink, blocks, u, nt, stream)
+                ev = G.Events(2)
+                torch.cuda.synchronize()
+                ev.record(0, stream)
+                for _ in range(reps):
+                    G.hbm_read_probe_ex(buf, sink, blocks, u, nt, stream)
+                ev.record(1, stream)
+                torch.cuda.synchronize()
+                gbps = nbytes * reps / (ev.elapsed(0, 1) * 1e-3) / 1e9
+                sweep.append({"blocks": blocks, "loads_in_flight": u, "nontemporal": nt, "gbps": gbps})
+        del sink
+    del buf
+    best = max(sweep, key=lambda r: r["gbps"])
+    return best["gbps"], sweep
 
 
 def bench_prefill(gpu, table, E, steps, warmup, seed=3, P=None, cpu_seconds=8.0, no_cpu=True):

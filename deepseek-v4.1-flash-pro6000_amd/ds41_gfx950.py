@@ -279,6 +279,16 @@ def hbm_read_probe(buf, sink, blocks, stream=None):
     check(f(buf.data_ptr(), buf.numel(), sink.data_ptr(), blocks, _stream(stream)), "ds41_hbm_read_probe")
 
 
+def hbm_read_probe_ex(buf, sink, blocks, loads_in_flight, nontemporal, stream=None):
+    """hbm_read_probe with loads_in_flight (4, 8, 16) 16-byte loads per thread in flight, plain or
+    non-temporal loads."""
+    f = lib().ds41_hbm_read_probe_ex
+    f.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                  ctypes.c_void_p]
+    check(f(buf.data_ptr(), buf.numel(), sink.data_ptr(), blocks, loads_in_flight, int(nontemporal),
+            _stream(stream)), "ds41_hbm_read_probe_ex")
+
+
 def layer_workspace_bytes(T, H, I, E, K):
     return lib().ds41_moe_layer_workspace_bytes(T, H, I, E, K)
 

@@ -586,6 +586,11 @@ const char *ds41_gfx950_version(void);
  * (device, blocks * 256 * 4 bytes). Timing it gives the practical HBM read
  * ceiling that the HBM-bound kernels' rates are compared against. */
 int ds41_hbm_read_probe(const void *buf, size_t bytes, void *sink, int blocks, void *stream);
+/* The same probe with loads_in_flight (4, 8 or 16) 16-byte loads in flight per thread and plain
+ * (nontemporal 0) or non-temporal (1) loads; sink holds blocks * 256 words. A caller sweeps
+ * these and the grid and takes the best rate as the device's read ceiling. */
+int ds41_hbm_read_probe_ex(const void *buf, size_t bytes, void *sink, int blocks, int loads_in_flight,
+                           int nontemporal, void *stream);
 /* Self-check of the device's E4M3 converter (no counterpart in the reference): the MXFP8
  * quantisers convert with the hardware instruction, which must round exactly as the integer
  * formulation of OCP E4M3 (round to nearest even, saturating) on every fp32 in [-448, 448].
