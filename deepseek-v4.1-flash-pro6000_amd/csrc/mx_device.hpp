@@ -302,8 +302,16 @@ struct XTileRound {
 #pragma unroll
     for (int j = 0; j < NS; ++j) asm volatile("" : "+v"(b[j]));
   }
+  __device__ __forceinline__ void store_presplit(uint8_t *lq, uint8_t *ls, const uint8_t *x, const uint8_t *xs, int k,
+                                                 int tokens) const;
+  // Presplit: the layout of stage_xtile_presplit (2 * T4 rows), else that of stage_xtile.
+  template <bool Presplit = false>
   __device__ __forceinline__ void store(uint8_t *lq, uint8_t *ls, const uint8_t *x, const uint8_t *xs, int k,
                                         int tokens) const {
+    if constexpr (Presplit) {
+      store_presplit(lq, ls, x, xs, k, tokens);
+      return;
+    }
     if (!ok) {
       stage_xtile(lq, ls, x, xs, k, tokens, [](int r) { return (size_t)r; });
       return;
@@ -330,6 +338,45 @@ struct XTileRound {
     }
   }
 };
+
+template <int NP, int NS>
+__device__ __forceinline__ void XTileRound<NP, NS>::store_presplit(uint8_t *lq, uint8_t *ls, const uint8_t *x,
+                                                                  const uint8_t *xs, int k, int tokens) const {
+  if (!ok) {
+    stage_xtile_presplit(lq, ls, x, xs, k, tokens, [](int r) { return (size_t)r; });
+    return;
+  }
+  const int stride = xtile_stride(k), sstride = xtile_sstride(k), pieces = (stride - 16) >> 4;
+  const int T4 = (tokens + 3) & ~3, nrows = 2 * T4, kp = k >> 4, nsrc = tokens * kp, ng = k >> 5;
+  const int bd = (int)blockDim.x;
+  const UDiv dkp((uint32_t)kp), dss((uint32_t)sstride);
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int p = (int)threadIdx.x + j * bd;
+    if (p >= nsrc) break;
+    const int t = (int)dkp.q((uint32_t)p), off = (p - t * kp) << 4;
+    const SplitLane big{t, 0u}, small{t, 0xffffffffu};
+    *reinterpret_cast<uint4 *>(lq + t * stride + off) = split_bytes(v[j], big);
+    *reinterpret_cast<uint4 *>(lq + (T4 + t) * stride + off) = split_bytes(v[j], small);
+  }
+  for (int p = threadIdx.x; p < nrows * pieces; p += bd) {  // trailing chunk, padding rows
+    const int r = p / pieces, pc = p - r * pieces, t = r < T4 ? r : r - T4;
+    if (pc >= kp || t >= tokens) *reinterpret_cast<uint4 *>(lq + r * stride + (pc << 4)) = make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {  // rows tokens..T4-1 of the scales (never loaded) are 127 too
+    const int p = (int)threadIdx.x + j * bd;
+    if (p >= T4 * sstride) break;
+    const int t = (int)dss.q((uint32_t)p), g = p - t * sstride;
+    const uint8_t e = g < ng && t < tokens ? (uint8_t)b[j] : (uint8_t)127;
+    ls[p] = e;
+    ls[T4 * sstride + p] = e;
+  }
+  for (int p = (int)threadIdx.x + NS * bd; p < T4 * sstride; p += bd) {  // past the loaded rows
+    ls[p] = (uint8_t)127;
+    ls[T4 * sstride + p] = (uint8_t)127;
+  }
+}
 
 // Pre-split staging: split_rows(tokens) LDS rows, row t = the |v| >= 1 bytes of
 // source row t and row T4 + t its |v| < 1 bytes (padding rows zero, scales
@@ -686,11 +733,19 @@ struct Gemv16F8 {
   int q, k, ng, c0, c1, nb;
   uint4 A[U][2], B[U][2];
   uint4 SA, SB;
+  // activation operands and scales of batches 0 / 1 (prefetch_x), with the tile row of this lane
+  uint4 XA[U][2], XB[U][2];
+  int XSA[U], XSB[U];
+  const uint8_t *xa_, *sa_;
+  SplitLane sl_;
 
+  // 16 weight bytes at `off`; a piece past the row (the partial last chunk) reads the row's last
+  // 16 bytes instead. Its activations are zero, so it adds nothing: 0 x a finite code is 0, and a
+  // NaN code there already makes the row's true sum NaN. The load is unconditional, so the wait
+  // counts of the loads issued before it (the activation tile's) stay exact.
   __device__ __forceinline__ uint4 piece(int off) const {
-    const int o = off < k ? off : 0;  // clamped address; the value is replaced below
-    const u32x4 v = *(global_u4u)(w + o);
-    return off < k ? make_uint4(v.x, v.y, v.z, v.w) : make_uint4(0, 0, 0, 0);
+    const u32x4 v = *(global_u4u)(w + (off < k ? off : k - 16));
+    return make_uint4(v.x, v.y, v.z, v.w);
   }
   // first K32 group of the 16-group scale window loaded for batch b
   __device__ __forceinline__ int window(int b) const {
@@ -698,6 +753,10 @@ struct Gemv16F8 {
     return g0 + 16 <= ng ? g0 : (ng >= 16 ? ng - 16 : 0);
   }
   __device__ __forceinline__ void load(uint4 (*buf)[2], uint4 &S, int b) const {
+    load_w(buf, b);
+    load_scales(S, b);
+  }
+  __device__ __forceinline__ void load_w(uint4 (*buf)[2], int b) const {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int c = c0 + b * U + u;
@@ -705,6 +764,8 @@ struct Gemv16F8 {
       buf[u][0] = piece(128 * c + 16 * q);
       buf[u][1] = piece(128 * c + 64 + 16 * q);
     }
+  }
+  __device__ __forceinline__ void load_scales(uint4 &S, int b) const {
     if (ng >= 16) {
       const u32x4 v = *(global_u4u)(sr + window(b));
       S = make_uint4(v.x, v.y, v.z, v.w);
@@ -721,16 +782,95 @@ struct Gemv16F8 {
     sr = srow;
     k = kk;
     ng = kk >> 5;
-    c0 = cbegin;
-    c1 = cend;
+    // the chunk range is the same for the whole wave: scalar registers, scalar branches
+    c0 = __builtin_amdgcn_readfirstlane(cbegin);
+    c1 = __builtin_amdgcn_readfirstlane(cend);
     nb = (c1 - c0 + U - 1) / U;
-    load(A, SA, 0);  // both batches in flight before the wave's turn in a chain
-    if (nb > 1) load(B, SB, 1);
+    // both batches in flight before the wave's turn in a chain: the scales first (their short-row
+    // form is a branch), then the weights unconditionally (a one-batch range reloads its last
+    // chunk), so that the wait counts of loads issued before these stay exact
+    load_scales(SA, 0);
+    load_scales(SB, 1);
+    load_w(A, 0);
+    load_w(B, 1);
   }
   __device__ __forceinline__ int scale_of(const uint4 &S, int b, int c) const {
     const int g = 4 * c + q, gc = g < ng ? g : ng - 1, idx = gc - window(b);
-    const uint32_t d = (idx >> 2) == 0 ? S.x : (idx >> 2) == 1 ? S.y : (idx >> 2) == 2 ? S.z : S.w;
-    return (int)((d >> (8 * (idx & 3))) & 0xffu);
+    // byte idx (0..15) of S with selects of values (not of member addresses, which would put the
+    // object in scratch) and a bit-field extract: no branches
+    const uint32_t sx = S.x, sy = S.y, sz = S.z, sw = S.w;
+    const uint32_t lo = (idx & 4) ? sy : sx, hi = (idx & 4) ? sw : sz, d = (idx & 8) ? hi : lo;
+    return (int)__builtin_amdgcn_ubfe(d, 8u * (uint32_t)(idx & 3), 8u);
+  }
+  // A operands and activation scales of batch b from the tile (chunks clamped as load() does).
+  template <bool Split>
+  __device__ __forceinline__ void xload(uint4 (*X)[2], int *XS, int b) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int c = c0 + b * U + u;
+      c = c < c1 ? c : (c1 > c0 ? c1 - 1 : 0);
+      uint4 lo = *reinterpret_cast<const uint4 *>(xa_ + 128 * c);
+      uint4 hi = *reinterpret_cast<const uint4 *>(xa_ + 128 * c + 64);
+      if (Split) {
+        lo = split_bytes(lo, sl_);
+        hi = split_bytes(hi, sl_);
+      }
+      X[u][0] = lo;
+      X[u][1] = hi;
+      XS[u] = sa_[4 * c];
+    }
+  }
+  // Reads the activation operands of the first two batches from the staged tile into registers
+  // (after the tile's barrier), for dots().
+  template <bool Split>
+  __device__ __forceinline__ void prefetch_x(const XTile &xt) {
+    sl_ = split_lane(threadIdx.x & 15, xt.tokens, Split);
+    xa_ = xt.q + sl_.src * xt.stride + 16 * q;
+    sa_ = xt.s + sl_.src * xt.sstride + q;
+    xload<Split>(XA, XSA, 0);
+    if (nb > 1) xload<Split>(XB, XSB, 1);
+  }
+  // With at most two batches (nb <= 2) and the operands prefetched: each chunk's scaled dot on its
+  // own (no accumulator chained through the MFMAs, so they issue back to back as soon as the
+  // weights land), for add_dots to add in ascending K during the wave's turn.
+  __device__ __forceinline__ void dots(v4f (&d)[2 * U]) const {
+    const v4f z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const v8i av = v8i{(int)XA[u][0].x, (int)XA[u][0].y, (int)XA[u][0].z, (int)XA[u][0].w,
+                         (int)XA[u][1].x, (int)XA[u][1].y, (int)XA[u][1].z, (int)XA[u][1].w};
+      const v8i bv = v8i{(int)A[u][0].x, (int)A[u][0].y, (int)A[u][0].z, (int)A[u][0].w,
+                         (int)A[u][1].x, (int)A[u][1].y, (int)A[u][1].z, (int)A[u][1].w};
+      d[u] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, z, 0, 0, 0, XSA[u], 0, scale_of(SA, 0, c0 + u));
+    }
+    if (nb < 2) return;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const v8i av = v8i{(int)XB[u][0].x, (int)XB[u][0].y, (int)XB[u][0].z, (int)XB[u][0].w,
+                         (int)XB[u][1].x, (int)XB[u][1].y, (int)XB[u][1].z, (int)XB[u][1].w};
+      const v8i bv = v8i{(int)B[u][0].x, (int)B[u][0].y, (int)B[u][0].z, (int)B[u][0].w,
+                         (int)B[u][1].x, (int)B[u][1].y, (int)B[u][1].z, (int)B[u][1].w};
+      d[U + u] =
+          __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, z, 0, 0, 0, XSB[u], 0, scale_of(SB, 1, c0 + U + u));
+    }
+  }
+  // Chunks past the wave's range (the clamped reloads of its last chunk) as +0, which leaves a
+  // sum unchanged, so the chain adds all 2U slots of every wave without a branch.
+  __device__ __forceinline__ void clear_past_range(v4f (&d)[2 * U]) const {
+    const v4f z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 2 * U; ++i)
+      if (c0 + i >= c1) d[i] = z;  // uniform
+  }
+  // acc plus the wave's chunk dots, one chunk after another in ascending K (after
+  // clear_past_range the slots past the range add +0).
+  __device__ __forceinline__ v4f add_dots(const v4f (&d)[2 * U], v4f acc) const {
+#pragma unroll
+    for (int i = 0; i < 2 * U; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = __fadd_rn(acc[r], d[i][r]);
+    }
+    return acc;
   }
   // Continues acc over the wave's chunk range.
   template <bool Split = false>
@@ -785,21 +925,59 @@ __device__ __forceinline__ void f8_chain_range(int k, int Wc, int j, int &c0, in
 // Runs a Wc-wave serial-carry chain: in turn t, wave j == t continues the
 // accumulator the previous wave left in `carry` (LDS, 64 lanes x 4 floats of
 // this chain). Every wave of the workgroup calls it (the turns synchronise the
-// workgroup); the returned value is valid in the chain's last wave.
-template <int Wc, bool Split>
+// workgroup); the returned value is valid in the chain's last wave. Wave j
+// passes j barriers, runs its turn, then passes the other Wc - j: barrier t
+// (1-based) separates turn t-1 from turn t, and the GEMV's code exists once.
+// Dots: every wave has at most two batches (f8_dots_fit) and the caller prefetched its operands
+// (prefetch_x). Each wave forms its chunk dots as soon as its weights land (Gemv16F8::dots);
+// waves 0..Wc-2 leave theirs in `carry` ([Wc-1][8 chunks][64 lanes] x 4 floats), and after one
+// barrier the last wave adds every chunk dot in ascending K: every 128-k chunk's dot is kept
+// apart and the chunks are added serially (the reference keeps every K32 dot apart and adds them
+// serially, components/dense/src/dense.cu:36-82; a chunk here is four K32 dots summed by the
+// MFMA). Otherwise (carry: 64 lanes x 4 floats) the turns run the MFMAs on the carried sum.
+template <int Wc, bool Split, bool Dots = false>
 __device__ __forceinline__ v4f f8_chain(Gemv16F8 &g, const XTile &xt, float *carry, int j) {
-  const int lane = threadIdx.x & 63;
+  constexpr int D = 2 * Gemv16F8::U;
+  const int lane = threadIdx.x & 63, jj = __builtin_amdgcn_readfirstlane(j);
   v4f acc = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (Dots) {
+    v4f d[D];
+    g.dots(d);
+    g.clear_past_range(d);
+    if (jj + 1 < Wc) {
 #pragma unroll
-  for (int t = 0; t < Wc; ++t) {
-    if (j == t) {
-      if (t) acc = *reinterpret_cast<const v4f *>(carry + 4 * lane);
-      acc = g.template run<Split>(xt, acc);
-      if (t + 1 < Wc) *reinterpret_cast<v4f *>(carry + 4 * lane) = acc;
+      for (int i = 0; i < D; ++i) *reinterpret_cast<v4f *>(carry + 4 * ((jj * D + i) * 64 + lane)) = d[i];
     }
     __syncthreads();
+    if (jj + 1 == Wc) {
+      v4f p[(Wc - 1) * D];  // every slot read at once, then added in order (+0 past a range)
+#pragma unroll
+      for (int i = 0; i < (Wc - 1) * D; ++i) p[i] = *reinterpret_cast<const v4f *>(carry + 4 * (i * 64 + lane));
+#pragma unroll
+      for (int i = 0; i < (Wc - 1) * D; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = __fadd_rn(acc[r], p[i][r]);
+      }
+      acc = g.add_dots(d, acc);
+    }
+    return acc;
+  } else {
+    for (int t = 0; t < jj; ++t) __syncthreads();
+    if (jj) acc = *reinterpret_cast<const v4f *>(carry + 4 * lane);
+    acc = g.template run<Split>(xt, acc);
+    if (jj + 1 < Wc) *reinterpret_cast<v4f *>(carry + 4 * lane) = acc;
+    for (int t = jj; t < Wc; ++t) __syncthreads();
+    return acc;
   }
-  return acc;
+}
+// LDS bytes of f8_chain's carry for one chain.
+__host__ __device__ __forceinline__ constexpr size_t f8_carry_bytes(int Wc, bool dots) {
+  return dots ? (size_t)(Wc - 1) * 8 * 64 * 16 : (size_t)64 * 16;
+}
+// Whether every wave of a Wc-wave chain over a k-long row has at most two batches of chunks.
+__host__ __device__ __forceinline__ bool f8_dots_fit(int k, int Wc) {
+  const int nch = ((k >> 5) + 3) >> 2;
+  return (nch + Wc - 1) / Wc <= 2 * Gemv16F8::U;
 }
 
 // Workgroup barrier that orders LDS accesses only. __syncthreads() also

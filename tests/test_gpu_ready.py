@@ -4,11 +4,12 @@
 Bars:
 - flags that already hold each expert's generation give output bits identical to ready == NULL,
   for the verify layer (gate/up, fused down + reduce) and the grouped projection API;
-- flags written by a copy on another stream after the layer is queued: the kernels wait for them,
-  the status word stays 0 and the output bits are again identical;
+- flags written by the host after the layer is queued: the kernels wait for them, the status word
+  stays 0 and the output bits are again identical;
 - a flag that the host never sets (the bounded wait's failure path, forced from the host): status
   bit 1 is raised, every output that needed the expert is NaN and the others are unchanged. The
   wait gives up after 2 s of the device's wall clock, so every kernel still exits."""
+import ctypes
 import time
 
 import numpy as np
@@ -20,14 +21,25 @@ pytestmark = pytest.mark.gpu
 
 
 def _flagged(experts, flags, gen):
-    """Copies of the expert dicts whose table entries carry ready = &flags[i], generation gen[i]."""
+    """Copies of the expert dicts whose table entries carry ready = &flags[i], generation gen[i]
+    (flags: a tensor or the address of a uint32 array)."""
+    base = flags if isinstance(flags, int) else flags.data_ptr()
     out = []
     for i, e in enumerate(experts):
         d = dict(e)
-        d["ready"] = flags.data_ptr() + 4 * i
+        d["ready"] = base + 4 * i
         d["generation"] = int(gen[i])
         out.append(d)
     return out
+
+
+def _loaded_hip():
+    """The HIP runtime this process already runs (torch's copy): a second copy of the runtime
+    loaded beside it would own streams the first one cannot use."""
+    with open("/proc/self/maps") as f:
+        paths = {ln.split()[-1] for ln in f if "libamdhip64.so" in ln}
+    assert len(paths) == 1, paths
+    return ctypes.CDLL(paths.pop())
 
 
 def _layer_inputs(gpu, T, H, E, seed):
@@ -90,31 +102,42 @@ def test_ready_flags_already_set_match_no_flags(gpu):
     assert np.array_equal(host(outs[0]), host(outs[1]))
 
 
-def test_ready_flags_written_by_another_stream(gpu):
-    """The layer is queued first; the flags arrive from pinned host memory on a second stream."""
+def test_ready_flags_written_after_the_layer_is_queued(gpu):
+    """The layer is queued first and its kernels wait; the host then writes the flags. The flags sit
+    in coherent pinned host memory, which the kernels' polls read through to, so no copy has to get
+    past the waiting kernels: HIP maps a process's streams onto a few hardware queues, and a copy on
+    a stream that shares the waiting kernel's queue would run only after it."""
     import torch
     import ds41_gfx950 as G
     T, H, I, E, K = 4, 2048, 1024, 48, 6
-    say(f"ready flags from another stream: layer T={T} H={H} I={I} E={E}")
+    say(f"ready flags written after queueing: layer T={T} H={H} I={I} E={E}")
     P, experts = make_layer(gpu, 54, H, I, E, T)
     gen = (np.arange(E + 1, dtype=np.uint32) + 1) * 5
-    flags = torch.zeros(E + 1, dtype=torch.int32, device=gpu)
-    plain, _ = G.device_table(experts, gpu)
-    flagged, _ = G.device_table(_flagged(experts, flags, gen), gpu)
-    x, wg, bias = _layer_inputs(gpu, T, H, E, 55)
-    y0, _, _ = _run_layer(gpu, plain, x, wg, bias, T, H, I, E, K)
-    torch.cuda.synchronize()
-    src = torch.from_numpy(gen.astype(np.int32)).pin_memory()
-    compute, copy = torch.cuda.Stream(), torch.cuda.Stream()  # default priority, non-blocking
-    t0 = time.time()
-    y1, _, ws = _run_layer(gpu, flagged, x, wg, bias, T, H, I, E, K, stream=compute)
-    with torch.cuda.stream(copy):
-        flags.copy_(src, non_blocking=True)
-    torch.cuda.synchronize()
-    dt = time.time() - t0
-    say(f"  layer with flags set after queueing finished in {dt * 1e3:.1f} ms")
-    assert G.take_status() == 0
-    assert np.array_equal(host(y0), host(y1))
+    hip = _loaded_hip()
+    hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+    hip.hipHostFree.argtypes = [ctypes.c_void_p]
+    raw = ctypes.c_void_p()
+    assert hip.hipHostMalloc(ctypes.byref(raw), 4 * (E + 1), 0x40000000) == 0  # hipHostMallocCoherent
+    try:
+        flags = np.ctypeslib.as_array((ctypes.c_uint32 * (E + 1)).from_address(raw.value))
+        flags[:] = 0
+        plain, _ = G.device_table(experts, gpu)
+        flagged, _ = G.device_table(_flagged(experts, raw.value, gen), gpu)
+        x, wg, bias = _layer_inputs(gpu, T, H, E, 55)
+        y0, _, _ = _run_layer(gpu, plain, x, wg, bias, T, H, I, E, K)
+        torch.cuda.synchronize()
+        t0 = time.time()
+        y1, _, ws = _run_layer(gpu, flagged, x, wg, bias, T, H, I, E, K)
+        time.sleep(0.05)  # the kernels are waiting by now
+        flags[:] = gen
+        torch.cuda.synchronize()
+        dt = time.time() - t0
+        say(f"  layer with flags set after queueing finished in {dt * 1e3:.1f} ms")
+        assert G.take_status() == 0
+        assert np.array_equal(host(y0), host(y1))
+    finally:
+        torch.cuda.synchronize()
+        hip.hipHostFree(raw.value)
 
 
 @pytest.mark.parametrize("H", [512, 1024])
