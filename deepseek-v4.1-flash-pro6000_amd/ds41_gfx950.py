@@ -31,8 +31,24 @@ class GemmJob(ctypes.Structure):
                 ("output", ctypes.c_void_p)]
 
 
-class MoeLayerArgs(ctypes.Structure):
-    _fields_ = [("x_bf16", ctypes.c_void_p), ("router_w", ctypes.c_void_p),
+ABI_VERSION = 1  # DS41_GFX950_ABI_VERSION
+_ABI_FIELDS = [("abi_version", ctypes.c_uint32), ("struct_bytes", ctypes.c_uint32)]
+
+
+class _Versioned(ctypes.Structure):
+    """A struct that begins with abi_version and struct_bytes (filled in here; the other fields
+    follow positionally or by name)."""
+
+    def __init__(self, *args, **kw):
+        super().__init__(ABI_VERSION, ctypes.sizeof(type(self)), *args, **kw)
+
+    @classmethod
+    def data_fields(cls):
+        return [f for f, _ in cls._fields_ if f not in ("abi_version", "struct_bytes")]
+
+
+class MoeLayerArgs(_Versioned):
+    _fields_ = _ABI_FIELDS + [("x_bf16", ctypes.c_void_p), ("router_w", ctypes.c_void_p),
                 ("router_bias", ctypes.c_void_p), ("table", ctypes.c_void_p),
                 ("expert_base", ctypes.c_int32), ("shared_index", ctypes.c_int32),
                 ("tokens", ctypes.c_int32), ("hidden", ctypes.c_int32),
@@ -66,15 +82,15 @@ class StackLayer(ctypes.Structure):
                 ("host_slab_count", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
-class StackDesc(ctypes.Structure):
-    _fields_ = [("layers", ctypes.c_int32), ("max_tokens", ctypes.c_int32), ("hidden", ctypes.c_int32),
+class StackDesc(_Versioned):
+    _fields_ = _ABI_FIELDS + [("layers", ctypes.c_int32), ("max_tokens", ctypes.c_int32), ("hidden", ctypes.c_int32),
                 ("inter", ctypes.c_int32), ("n_experts", ctypes.c_int32), ("topk", ctypes.c_int32),
                 ("score_mode", ctypes.c_int32), ("route_scale", ctypes.c_float), ("swiglu_limit", ctypes.c_float),
                 ("layer", ctypes.POINTER(StackLayer)), ("weight_layout", ctypes.c_int32)]
 
 
-class StackStats(ctypes.Structure):
-    _fields_ = [("steps", ctypes.c_uint64), ("layers", ctypes.c_uint64), ("resident_routed", ctypes.c_uint64),
+class StackStats(_Versioned):
+    _fields_ = _ABI_FIELDS + [("steps", ctypes.c_uint64), ("layers", ctypes.c_uint64), ("resident_routed", ctypes.c_uint64),
                 ("host_fetched", ctypes.c_uint64), ("h2d_bytes", ctypes.c_uint64),
                 ("invalid_layers", ctypes.c_uint64), ("cached_routed", ctypes.c_uint64)]
 
@@ -575,8 +591,8 @@ class HostSlabs:
             pass
 
 
-class CacheStats(ctypes.Structure):
-    _fields_ = [("requests", ctypes.c_uint64), ("hits", ctypes.c_uint64), ("misses", ctypes.c_uint64),
+class CacheStats(_Versioned):
+    _fields_ = _ABI_FIELDS + [("requests", ctypes.c_uint64), ("hits", ctypes.c_uint64), ("misses", ctypes.c_uint64),
                 ("evictions", ctypes.c_uint64), ("h2d_bytes", ctypes.c_uint64), ("slots", ctypes.c_uint64),
                 ("prefetch_requests", ctypes.c_uint64), ("prefetch_copies", ctypes.c_uint64)]
 
@@ -642,12 +658,12 @@ class VerifyStack:
     def cache_stats(self):
         st = CacheStats()
         check(lib().ds41_verify_stack_cache_stats(self.handle, ctypes.byref(st)), "ds41_verify_stack_cache_stats")
-        return {f: int(getattr(st, f)) for f, _ in CacheStats._fields_}
+        return {f: int(getattr(st, f)) for f in CacheStats.data_fields()}
 
     def stats(self):
         st = StackStats()
         check(lib().ds41_verify_stack_stats(self.handle, ctypes.byref(st)), "ds41_verify_stack_stats")
-        return {f: int(getattr(st, f)) for f, _ in StackStats._fields_}
+        return {f: int(getattr(st, f)) for f in StackStats.data_fields()}
 
     def close(self):
         if self.handle:
@@ -916,8 +932,8 @@ class Records:
 
 
 # ---- MTP drafter: routed-expert service and router top-3 -------------------------------
-class TargetExpertsDesc(ctypes.Structure):
-    _fields_ = [("table", ctypes.c_void_p), ("expert_base", ctypes.c_int32), ("hidden", ctypes.c_int32),
+class TargetExpertsDesc(_Versioned):
+    _fields_ = _ABI_FIELDS + [("table", ctypes.c_void_p), ("expert_base", ctypes.c_int32), ("hidden", ctypes.c_int32),
                 ("inter", ctypes.c_int32), ("swiglu_limit", ctypes.c_float), ("check_routes", ctypes.c_int32),
                 ("stream", ctypes.c_void_p), ("stage_events", ctypes.c_void_p), ("weight_layout", ctypes.c_int32)]
 

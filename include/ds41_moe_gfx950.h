@@ -127,7 +127,18 @@ int ds41_router_topk(const float *b, int32_t *ids, int M, int N, int topk, void 
  * table[shared_index] (shared_index < 0: none). hidden % 256 == 0 (<= 8192),
  * inter % 32 == 0, n_experts <= 512, topk <= 8.
  * Calls that share one workspace must be ordered (same stream). */
+/* Size and version negotiation of the structs that grow between builds (the reference's C structs
+ * carry the same pair, engine/include/ds41/target_shared.h:11-13): ds41_moe_layer_args,
+ * ds41_stack_desc, ds41_stack_stats, ds41_cache_stats and ds41_target_experts_desc begin with
+ * abi_version and struct_bytes. The caller sets them (DS41_ABI_INIT(T) for the first two
+ * initialisers) on the structs it passes in and on those it passes to be filled; the library
+ * rejects any other pair with hipErrorInvalidValue before it reads or writes past those two
+ * fields. */
+#define DS41_GFX950_ABI_VERSION 1u
+#define DS41_ABI_INIT(T) DS41_GFX950_ABI_VERSION, (uint32_t)sizeof(T)
 typedef struct ds41_moe_layer_args {
+  uint32_t abi_version;            /* DS41_GFX950_ABI_VERSION */
+  uint32_t struct_bytes;           /* sizeof this struct as the caller was built */
   const void *x_bf16;             /* [tokens][hidden] */
   const float *router_w;          /* [n_experts][hidden] fp32 */
   const float *router_bias;       /* [n_experts] fp32 */
@@ -278,6 +289,8 @@ typedef struct ds41_stack_layer {
 } ds41_stack_layer;
 
 typedef struct ds41_stack_desc {
+  uint32_t abi_version;            /* DS41_GFX950_ABI_VERSION */
+  uint32_t struct_bytes;           /* sizeof this struct as the caller was built */
   int32_t layers, max_tokens, hidden, inter, n_experts, topk, score_mode;
   float route_scale, swiglu_limit;
   const ds41_stack_layer *layer;   /* host array [layers], copied at create */
@@ -287,6 +300,8 @@ typedef struct ds41_stack_desc {
 
 /* Cumulative counters of the layers that have a host tier (read back each layer). */
 typedef struct ds41_stack_stats {
+  uint32_t abi_version;            /* DS41_GFX950_ABI_VERSION */
+  uint32_t struct_bytes;           /* sizeof this struct as the caller was built */
   uint64_t steps, layers;          /* layers = layer passes with a host tier */
   uint64_t resident_routed;        /* routed experts served from their table's HBM slabs (shared excluded) */
   uint64_t host_fetched;           /* host-tier experts copied in (on demand or by a prefetch) */
@@ -463,6 +478,8 @@ int ds41_drift_destroy(void *drift);
  * experts come from each layer's table. Expert id of layer l, expert e: l * n_experts + e. */
 int ds41_verify_stack_cache(void *stack, int slots, const ds41_placement *policy);
 typedef struct ds41_cache_stats {
+  uint32_t abi_version;            /* DS41_GFX950_ABI_VERSION */
+  uint32_t struct_bytes;           /* sizeof this struct as the caller was built */
   uint64_t requests;                 /* routed host-tier experts served through the cache */
   uint64_t hits, misses, evictions;  /* hits include experts a prefetch brought in */
   uint64_t h2d_bytes;                /* demand and prefetch copies */
@@ -533,6 +550,8 @@ int ds41_record_load_slab(void *records, int index, int hidden, int inter, void 
  * components/moe/include/ds41/store.hpp:16) are table[expert_base + 128 * s + id],
  * id 0..127. */
 typedef struct ds41_target_experts_desc {
+  uint32_t abi_version;            /* DS41_GFX950_ABI_VERSION */
+  uint32_t struct_bytes;           /* sizeof this struct as the caller was built */
   const ds41_device_expert *table; /* device; every drafter expert resident in HBM */
   int32_t expert_base;             /* table index of stage 0, expert 0 */
   int32_t hidden, inter;           /* 5120, 2304 for the drafter */

@@ -53,7 +53,7 @@ def test_stack_abi_host_checks():
     import sys
     sys.path.insert(0, os.path.join(ROOT, "deepseek-v4.1-flash-pro6000_amd"))
     import ds41_gfx950 as G
-    assert ctypes.sizeof(G.StackLayer) == 56 and ctypes.sizeof(G.StackStats) == 56
+    assert ctypes.sizeof(G.StackLayer) == 56 and ctypes.sizeof(G.StackStats) == 64
     off, slab = G.slab_layout(4096, 2880)
     # the reference's offload slot: 18,800,640 B per expert (gate/up/down weights + e8m0 scales)
     assert slab == 18800640 and off == [0, 5898240, 6266880, 12165120, 12533760, 18432000]
@@ -78,8 +78,8 @@ def test_target_experts_abi_host_checks():
     import sys
     sys.path.insert(0, os.path.join(ROOT, "deepseek-v4.1-flash-pro6000_amd"))
     import ds41_gfx950 as G
-    assert ctypes.sizeof(G.TargetExpertsDesc) == 56
-    assert G.TargetExpertsDesc.weight_layout.offset == 48
+    assert ctypes.sizeof(G.TargetExpertsDesc) == 64
+    assert G.TargetExpertsDesc.weight_layout.offset == 56
     lib = ctypes.CDLL(LIB)
     h = ctypes.c_void_p(0)
     d = G.TargetExpertsDesc(0, 0, 5120, 2304, 10.0, 0, None, None, 0)  # null table
@@ -104,3 +104,38 @@ def test_read_probe_host_checks():
     assert f(ctypes.c_void_p(256), 1000, ctypes.c_void_p(256), 4, None) != 0   # not a multiple of 16
     assert f(ctypes.c_void_p(264), 1024, ctypes.c_void_p(256), 4, None) != 0   # misaligned
     assert f(ctypes.c_void_p(256), 1024, ctypes.c_void_p(256), 0, None) != 0   # no workgroups
+
+
+def test_versioned_structs_lead_with_abi_pair():
+    """The structs that grow between builds begin with (abi_version, struct_bytes), the pair the
+    reference's C structs carry (engine/include/ds41/target_shared.h:11-13). The Python mirrors fill
+    it in; the header's layout puts it at offsets 0 and 4; a caller built against another layout is
+    rejected before any field past the pair is read (the device-side half of this check runs in
+    tests/test_gpu_moe.py::test_layer_args_abi_pair_checked)."""
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "deepseek-v4.1-flash-pro6000_amd"))
+    import ds41_gfx950 as G
+    for cls in (G.MoeLayerArgs, G.StackDesc, G.StackStats, G.CacheStats, G.TargetExpertsDesc):
+        assert cls.abi_version.offset == 0 and cls.struct_bytes.offset == 4, cls
+        v = cls()
+        assert v.abi_version == G.ABI_VERSION == 1 and v.struct_bytes == ctypes.sizeof(cls), cls
+        assert "abi_version" not in cls.data_fields() and "struct_bytes" not in cls.data_fields()
+    hdr = open(os.path.join(ROOT, "include", "ds41_moe_gfx950.h")).read()
+    assert "#define DS41_GFX950_ABI_VERSION 1u" in hdr
+    for name in ("ds41_moe_layer_args", "ds41_stack_desc", "ds41_stack_stats", "ds41_cache_stats",
+                 "ds41_target_experts_desc"):
+        body = hdr.split("typedef struct %s {" % name, 1)[1]
+        first = [ln.split(";")[0].split()[-1] for ln in body.splitlines()[1:3]]
+        assert first == ["abi_version", "struct_bytes"], (name, first)
+    # a descriptor from another build (other size or version) is rejected by the host checks
+    lib = ctypes.CDLL(LIB)
+    h = ctypes.c_void_p(0)
+    layers = (G.StackLayer * 1)()
+    for version, size in ((G.ABI_VERSION + 1, ctypes.sizeof(G.StackDesc)),
+                          (G.ABI_VERSION, ctypes.sizeof(G.StackDesc) - 8)):
+        desc = G.StackDesc(1, 4, 4096, 2880, 384, 6, 0, 1.5, 10.0, layers)
+        desc.abi_version, desc.struct_bytes = version, size
+        assert lib.ds41_verify_stack_create(ctypes.byref(desc), ctypes.byref(h)) == 1 and not h.value
+    st = G.StackStats()
+    st.abi_version = 0
+    assert lib.ds41_verify_stack_stats(ctypes.c_void_p(1), ctypes.byref(st)) == 1  # rejected before the handle is used

@@ -317,3 +317,35 @@ def test_moe_layer_topk_ties_lower_id_first(gpu):
     u, b = O.router_scores(lg, bias_np)
     assert np.array_equal(host(ids), O.topk(b, K))
     assert np.array_equal(host(ids), np.tile(np.array(tied[:K], np.int32), (T, 1)))
+
+
+def test_layer_args_abi_pair_checked(gpu):
+    """ds41_moe_layer_args from another build: a struct_bytes or abi_version this build does not
+    know is rejected (hipErrorInvalidValue) and launches nothing, on both verify-layer entries; the
+    same struct with this build's pair runs."""
+    import ctypes
+    import torch
+    import ds41_gfx950 as G
+    T, H, I, E, K = 2, 512, 256, 16, 4
+    say(f"layer args abi pair T={T} H={H} I={I} E={E}")
+    P, experts = make_layer(gpu, 81, H, I, E, T)
+    table, _ = G.device_table(experts, gpu)
+    rng = np.random.default_rng(82)
+    x = dev(rand_x(rng, T, H), gpu)
+    wg = dev((rng.standard_normal((E, H)) * 0.02).astype(np.float32), gpu)
+    bias = dev(np.zeros(E, np.float32), gpu)
+    y = torch.full((T, H), float("nan"), dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(G.layer_workspace_bytes(T, H, I, E, K), dtype=torch.uint8, device=gpu)
+    a = G.make_layer_args(x, wg, bias, table, 0, E, T, H, I, E, K, y, ws)
+    for version, size in ((G.ABI_VERSION + 1, ctypes.sizeof(G.MoeLayerArgs)),
+                          (G.ABI_VERSION, ctypes.sizeof(G.MoeLayerArgs) - 8), (0, 0)):
+        a.abi_version, a.struct_bytes = version, size
+        assert G.lib().ds41_moe_verify_layer(ctypes.byref(a), G._stream()) == 1
+        assert G.moe_layer_noalloc_rc(a) == 1
+    torch.cuda.synchronize()
+    assert np.all(np.isnan(O.bf16_to_f32(host(y))))  # nothing ran
+    a.abi_version, a.struct_bytes = G.ABI_VERSION, ctypes.sizeof(G.MoeLayerArgs)
+    G.moe_layer(a)
+    torch.cuda.synchronize()
+    assert G.take_status() == 0
+    assert not np.any(np.isnan(O.bf16_to_f32(host(y))))
