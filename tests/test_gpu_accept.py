@@ -247,3 +247,16 @@ def test_accept_top_p_vocabulary_rows_listed_path(gpu):
     for top_p in (0.95, 0.9, 0.5):
         got, want, _ = bonus_draws(gpu, x, 1.0, top_p, 6)
         assert got == want, top_p
+
+
+@pytest.mark.parametrize("cluster", [40, 200])
+def test_accept_top_p_cluster_of_adjacent_logits(gpu, cluster):
+    """`cluster` distinct logits one ulp apart from 5.0 upward (the rest far below) share every key
+    bit above the lowest ten, so the first pass leaves exactly that cluster in its crossing bin. With
+    40 the finish kernel resolves the range directly; with 200 it is more than the 64 it resolves
+    directly, so its histogram passes go on. Draws must be the host's either way."""
+    x = np.full((1, 4096), -30.0, np.float32)
+    x[0, 100:100 + cluster] = (np.float32(5.0).view(np.uint32) + np.arange(cluster, dtype=np.uint32)).view(np.float32)
+    got, want, _ = bonus_draws(gpu, x, 1.0, 0.5, 24)
+    assert got == want
+    assert all(100 <= t[0] < 100 + cluster for t in got)
