@@ -904,7 +904,10 @@ def bench_stack(gpu, steps, warmup, fill_steps, side_steps, cpu_seconds, no_cpu,
         if d["invalid_layers"] or G.take_status():
             raise AssertionError(f"stack {mode}: invalid routes or kernel status during the timed steps")
         served = d["resident_routed"] + d["cached_routed"]
-        hbm = (served + d["layers"]) * EXPERT_BYTES + d["layers"] * E * H * 4
+        # router rows read: with caller route ids a layer scores only its routed experts (a token's
+        # weights normalise over its own routed experts); router routing scores all E of them
+        router_rows = served + d["host_fetched"] if mode.startswith("zipf") else d["layers"] * E
+        hbm = (served + d["layers"]) * EXPERT_BYTES + router_rows * H * 4
         sec = ms * 1e-3 * nsteps
         routing = {"zipf": "Zipf(1.1) ids drawn fresh every step (4b), no cache",
                    "router": "router on chained activations (4a), no cache",
@@ -917,6 +920,7 @@ def bench_stack(gpu, steps, warmup, fill_steps, side_steps, cpu_seconds, no_cpu,
              "steps": nsteps, "ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / nsteps,
              "tokens_per_s": T / (ms * 1e-3),
              "hbm_bytes_per_step": hbm / nsteps, "hbm_gbps": hbm / sec / 1e9,
+             "router_rows_per_layer": router_rows / d["layers"],
              "hbm_frac": hbm / sec / 1e9 / PEAK_HBM_GBPS,
              "h2d_bytes_per_step": d["h2d_bytes"] / nsteps, "h2d_gbps": d["h2d_bytes"] / sec / 1e9,
              "resident_routed_per_layer": d["resident_routed"] / d["layers"],
