@@ -965,7 +965,7 @@ def bench_stack(gpu, steps, warmup, fill_steps, side_steps, cpu_seconds, no_cpu,
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20, help="timed 40-layer steps of the headline leg")
+    ap.add_argument("--steps", type=int, default=100, help="timed 40-layer steps of the headline leg")
     ap.add_argument("--warmup", type=int, default=5, help="untimed warmup steps before every stack leg")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
